@@ -1,0 +1,62 @@
+"""Build the HIP shared library ``gbxcule_amd/lib/libgbx_hip.so`` for gfx950.
+
+``hipcc`` cross-compiles for gfx950 without a GPU present.  All HIP sources are
+compiled with packed FP32 instructions disabled (``-packed-fp32-ops``).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB_DIR = PKG / "lib"
+LIB_PATH = LIB_DIR / "libgbx_hip.so"
+SOURCES = ("gbx_step.hip", "gbx_aux.hip", "gbx_api.hip")
+ARCH = os.environ.get("GBX_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; the HIP library cannot be built")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source and link the shared library (always rebuilds)."""
+    LIB_DIR.mkdir(exist_ok=True)
+    tmp = LIB_DIR / "libgbx_hip.so.tmp"
+    cmd = [
+        hipcc(),
+        "-O3",
+        f"--offload-arch={ARCH}",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Xclang",
+        "-target-feature",
+        "-Xclang",
+        "-packed-fp32-ops",
+        "-I",
+        str(PKG.parent / "include"),
+        "-o",
+        str(tmp),
+        *[str(CSRC / s) for s in SOURCES],
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building libgbx_hip.so")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,353 @@
+// gbx_aux.hip -- kernels around the step: power-on fill, the 2x-downsampled
+// snapshot renderer, reset snapshot / masked restore, RAM-sense gather, state
+// hash, and the layout converters behind the export/import helpers.
+#include "gbx_aux.h"
+
+namespace gbx {
+namespace {
+
+__device__ __forceinline__ uint32_t block_of(uint32_t e) {
+  return __builtin_amdgcn_readfirstlane(e >> kEnvBlockShift);
+}
+
+// ---------------------------------------------------------------------------
+// Power-on memory image: zero everywhere except the boot image at 0x00-0xFF
+// (reference backends/warp_vec.py:335-340).  One thread per 16 bytes; the 16
+// bytes are 16 lanes of one address row, so they share one value.
+// ---------------------------------------------------------------------------
+__global__ void fill_mem_kernel(uint4* mem, size_t n16, const uint8_t* boot) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n16) return;
+  const uint32_t addr = (uint32_t)((i * 16) >> kEnvBlockShift) & 0xFFFFu;
+  uint32_t v = 0;
+  if (addr < 0x100u) v = (uint32_t)boot[addr] * 0x01010101u;
+  mem[i] = make_uint4(v, v, v, v);
+}
+
+__global__ void init_state_kernel(int32_t* cs, int32_t* sc, int npad, int mbc_kind) {
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (uint32_t)npad) return;
+  for (int k = 0; k < kCartStateStride; ++k) cs[cs_index(e, k)] = 0;
+  cs[cs_index(e, CS_MBC_KIND)] = mbc_kind;
+  cs[cs_index(e, CS_ROM_BANK_LO)] = 1;
+  cs[cs_index(e, CS_BOOTROM_ENABLED)] = 1;
+  for (int k = 0; k < kNumFields; ++k) sc[sc_index(e, k)] = 0;
+  sc[sc_index(e, F_JOYP_SELECT)] = 0x30;
+}
+
+// ---------------------------------------------------------------------------
+// Snapshot renderer (reference kernels/ppu_render_downsampled.py:27-234).
+// One thread per (env, output row); lanes of a wavefront are consecutive envs
+// of one row, so IO/OAM/tile-map reads of the same address coalesce.  The
+// row's sprite set (first 10 OAM entries overlapping the line, counted before
+// the x test) is selected once per row instead of once per sample.
+// ---------------------------------------------------------------------------
+struct Row {
+  const uint8_t* mb;  // block base
+  uint32_t lane;
+  __device__ uint32_t M(uint32_t addr) const { return mb[((size_t)addr << kEnvBlockShift) | lane]; }
+};
+
+__device__ uint32_t tile_pixel(const Row& r, uint32_t tile_addr, uint32_t row, uint32_t bit) {
+  const uint32_t lo = r.M(tile_addr + row * 2u), hi = r.M(tile_addr + row * 2u + 1u);
+  return (((hi >> bit) & 1u) << 1) | ((lo >> bit) & 1u);
+}
+
+__device__ uint32_t bg_tile_addr(uint32_t lcdc, uint32_t tile_id) {
+  if (lcdc & 0x10u) return 0x8000u + tile_id * 16u;
+  return (uint32_t)(0x9000 + ((int)tile_id >= 128 ? (int)tile_id - 256 : (int)tile_id) * 16);
+}
+
+__global__ void render_kernel(DevState s, uint8_t* out, int64_t base, int packed) {
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t oy = blockIdx.y;
+  if (e >= (uint32_t)s.n) return;
+  Row r{s.mem + ((size_t)block_of(e) << 22), e & (kEnvBlock - 1)};
+  const uint32_t y = oy * 2u;
+  const uint32_t lcdc = r.M(0xFF40), scy = r.M(0xFF42), scx = r.M(0xFF43);
+  const uint32_t bgp = r.M(0xFF47), obp0 = r.M(0xFF48), obp1 = r.M(0xFF49);
+  const uint32_t wy = r.M(0xFF4A), wx = r.M(0xFF4B);
+  const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
+  uint64_t sel = 0;
+  if (lcdc & 0x02u) {
+    uint32_t on_line = 0;
+    for (uint32_t k = 0; k < 40u; ++k) {
+      const uint32_t sy = r.M(0xFE00u + 4u * k), sx = r.M(0xFE01u + 4u * k);
+      if (sx == 0 || sy == 0 || sx >= 168u || sy >= 160u) continue;
+      const int top = (int)sy - 16;
+      if ((int)y < top || (int)y >= top + (int)height) continue;
+      if (on_line >= 10u) continue;
+      ++on_line;
+      sel |= 1ull << k;
+    }
+  }
+  const bool win = (lcdc & 0x20u) && y >= wy;
+  uint32_t word = 0;
+  const int nsamp = kDsW;
+  uint8_t* dst = out + base + (size_t)e * (packed ? (size_t)kDsWB * kDsH : (size_t)kDsW * kDsH) +
+                 (size_t)oy * (packed ? kDsWB : kDsW);
+  const bool aligned = (((uintptr_t)dst) & 3u) == 0;
+  for (int ox = 0; ox < nsamp; ++ox) {
+    const uint32_t x = (uint32_t)ox * 2u;
+    uint32_t shade = 0, bg_color = 0;
+    if (lcdc & 0x01u) {
+      uint32_t px, py, map;
+      if (win && (int)x >= (int)wx - 7) {
+        px = (x - (wx - 7u)) & 0xFFu;
+        py = (y - wy) & 0xFFu;
+        map = (lcdc & 0x40u) ? 0x9C00u : 0x9800u;
+      } else {
+        px = (x + scx) & 0xFFu;
+        py = (y + scy) & 0xFFu;
+        map = (lcdc & 0x08u) ? 0x9C00u : 0x9800u;
+      }
+      const uint32_t tile_id = r.M(map + (py >> 3) * 32u + (px >> 3));
+      bg_color = tile_pixel(r, bg_tile_addr(lcdc, tile_id), py & 7u, 7u - (px & 7u));
+      shade = (bgp >> (bg_color * 2u)) & 3u;
+    }
+    if (sel) {
+      bool found = false;
+      int best_x = 0;
+      uint32_t best_color = 0, best_attr = 0;
+      // OAM order: ties on x keep the lower index, as the reference does
+      for (uint64_t m = sel; m; m &= m - 1) {
+        const uint32_t k = (uint32_t)__builtin_ctzll(m);
+        const int left = (int)r.M(0xFE01u + 4u * k) - 8;
+        if ((int)x < left || (int)x >= left + 8) continue;
+        const int top = (int)r.M(0xFE00u + 4u * k) - 16;
+        uint32_t tile = r.M(0xFE02u + 4u * k);
+        const uint32_t attr = r.M(0xFE03u + 4u * k);
+        uint32_t row = (uint32_t)((int)y - top);
+        if ((attr >> 6) & 1u) row = height - 1u - row;
+        if (height == 16u) {
+          tile &= 0xFEu;
+          if (row >= 8u) {
+            tile += 1u;
+            row -= 8u;
+          }
+        }
+        const uint32_t pxl = (uint32_t)((int)x - left);
+        const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
+        const uint32_t color = tile_pixel(r, 0x8000u + tile * 16u, row, bit);
+        if (color == 0) continue;
+        if (!found || left < best_x) {
+          found = true;
+          best_x = left;
+          best_color = color;
+          best_attr = attr;
+        }
+      }
+      if (found && !(((best_attr >> 7) & 1u) && bg_color != 0)) {
+        const uint32_t pal = ((best_attr >> 4) & 1u) ? obp1 : obp0;
+        shade = (pal >> (best_color * 2u)) & 3u;
+      }
+    }
+    if (packed) {
+      word |= shade << (2u * (ox & 3) + 8u * ((ox >> 2) & 3));
+      if ((ox & 15) == 15 || ox == nsamp - 1) {
+        const int b0 = (ox >> 2) & ~3;  // first byte of this word
+        const int nb = (ox >> 2) - b0 + 1;
+        if (aligned && nb == 4) {
+          *reinterpret_cast<uint32_t*>(dst + b0) = word;
+        } else {
+          for (int q = 0; q < nb; ++q) dst[b0 + q] = (uint8_t)(word >> (8 * q));
+        }
+        word = 0;
+      }
+    } else {
+      word |= shade << (8u * (ox & 3));
+      if ((ox & 3) == 3) {
+        if (aligned) *reinterpret_cast<uint32_t*>(dst + (ox & ~3)) = word;
+        else
+          for (int q = 0; q < 4; ++q) dst[(ox & ~3) + q] = (uint8_t)(word >> (8 * q));
+        word = 0;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reset snapshot (core/reset_cache.py:68-190): one env into env-major buffers.
+// ---------------------------------------------------------------------------
+__global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int with_pix) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (uint32_t)kMemSize) snap.mem[i] = s.mem[mem_index(env, i)];
+  if (i < (uint32_t)s.cram_stride) snap.cram[i] = s.cram[cram_index(env, i, (uint32_t)s.cram_stride)];
+  if (i < (uint32_t)kSerialMax) snap.serial[i] = s.serial[(size_t)env * kSerialMax + i];
+  if (with_pix && i < (uint32_t)(kDsW * kDsH)) snap.pix[i] = s.pix[(size_t)env * kDsW * kDsH + i];
+  if (i < (uint32_t)kCartStateStride) snap.cs[i] = s.cs[cs_index(env, (int)i)];
+  if (i < (uint32_t)kNumFields)
+    snap.sc[i] = i == (uint32_t)F_ACTIONS ? s.actions[env] : s.sc[sc_index(env, (int)i)];
+  if (i < 2u) snap.cnt[i] = s.cnt[cnt_index(env, (int)i)];
+}
+
+// Masked restore of the interleaved images (mem + cart RAM).  Thread = (env,
+// chunk of addresses); unmasked lanes leave at once, so wavefronts with no
+// masked env cost nothing beyond their launch.
+constexpr uint32_t kResetChunk = 1024;
+__global__ void masked_mem_kernel(DevState s, const uint8_t* snap_mem, const uint8_t* snap_cram,
+                                  const uint8_t* mask) {
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (uint32_t)s.n || !mask[e]) return;
+  const uint32_t chunk = blockIdx.y;
+  const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
+  const uint32_t a0 = chunk * kResetChunk;
+  for (uint32_t a = a0; a < a0 + kResetChunk && a < per_env; ++a) {
+    if (a < (uint32_t)kMemSize) s.mem[mem_index(e, a)] = snap_mem[a];
+    else {
+      const uint32_t off = a - (uint32_t)kMemSize;
+      s.cram[cram_index(e, off, (uint32_t)s.cram_stride)] = snap_cram[off];
+    }
+  }
+}
+
+__global__ void masked_state_kernel(DevState s, SnapState snap, const uint8_t* mask, int with_pix) {
+  const uint32_t e = blockIdx.x;  // one block per env, threads over bytes
+  if (e >= (uint32_t)s.n || !mask[e]) return;
+  const uint32_t t = threadIdx.x;
+  for (uint32_t i = t; i < (uint32_t)kSerialMax; i += blockDim.x)
+    s.serial[(size_t)e * kSerialMax + i] = snap.serial[i];
+  if (with_pix)
+    for (uint32_t i = t; i < (uint32_t)(kDsW * kDsH); i += blockDim.x)
+      s.pix[(size_t)e * kDsW * kDsH + i] = snap.pix[i];
+  if (t < (uint32_t)kCartStateStride) s.cs[cs_index(e, (int)t)] = snap.cs[t];
+  if (t < (uint32_t)kNumFields) s.sc[sc_index(e, (int)t)] = snap.sc[t];
+  if (t < 2u) s.cnt[cnt_index(e, (int)t)] = snap.cnt[t];
+  if (t == 0) s.actions[e] = snap.sc[F_ACTIONS];
+}
+
+// RAM senses: out[e*k + j] = raw byte addrs[j] of env e.
+__global__ void gather_kernel(DevState s, const uint16_t* addrs, int k, uint8_t* out) {
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (uint32_t)s.n) return;
+  const uint8_t* mb = s.mem + ((size_t)block_of(e) << 22);
+  const uint32_t lane = e & (kEnvBlock - 1);
+  for (int j = 0; j < k; ++j)
+    out[(size_t)e * k + j] = mb[((size_t)addrs[j] << kEnvBlockShift) | lane];
+}
+
+// Per-env linear hash: sum of byte * K[addr] over memory, plus the scalar
+// fields, counters and cartridge state weighted by further K entries
+// (wrapping uint64 arithmetic; K = splitmix64(index)).
+__global__ void hash_kernel(DevState s, const uint64_t* K, uint64_t* out) {
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (uint32_t)s.n) return;
+  const uint8_t* mb = s.mem + ((size_t)block_of(e) << 22);
+  const uint32_t lane = e & (kEnvBlock - 1);
+  uint64_t h = 0;
+  for (uint32_t a = 0; a < (uint32_t)kMemSize; ++a)
+    h += (uint64_t)mb[((size_t)a << kEnvBlockShift) | lane] * K[a];
+  for (int f = 0; f < kNumFields; ++f) {
+    if (f == F_INSTR || f == F_CYCLES) continue;
+    const int32_t v = f == F_ACTIONS ? s.actions[e] : s.sc[sc_index(e, f)];
+    h += (uint64_t)(uint32_t)v * K[kMemSize + f];
+  }
+  h += (uint64_t)s.cnt[cnt_index(e, 0)] * K[kMemSize + F_INSTR];
+  h += (uint64_t)s.cnt[cnt_index(e, 1)] * K[kMemSize + F_CYCLES];
+  for (int k = 0; k < kCartStateStride; ++k)
+    h += (uint64_t)(uint32_t)s.cs[cs_index(e, k)] * K[kMemSize + 64 + k];
+  out[e] = h;
+}
+
+// Layout converters for the synchronous export/import helpers.
+__global__ void export_mem_kernel(DevState s, uint32_t env_lo, uint32_t count, uint32_t lo,
+                                  uint32_t len, uint8_t* dst) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)count * len) return;
+  const uint32_t ei = (uint32_t)(i / len), a = lo + (uint32_t)(i % len);
+  dst[i] = s.mem[mem_index(env_lo + ei, a)];
+}
+__global__ void import_mem_kernel(DevState s, uint32_t env, uint32_t addr, uint32_t len,
+                                  const uint8_t* src) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= len) return;
+  s.mem[mem_index(env, addr + i)] = src[i];
+}
+__global__ void export_cram_kernel(DevState s, uint32_t env_lo, uint32_t count, uint8_t* dst) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t stride = (uint32_t)s.cram_stride;
+  if (i >= (size_t)count * stride) return;
+  const uint32_t ei = (uint32_t)(i / stride), off = (uint32_t)(i % stride);
+  dst[i] = s.cram[cram_index(env_lo + ei, off, stride)];
+}
+
+}  // namespace
+
+hipError_t launch_reset(const DevState& s, hipStream_t st) {
+  const size_t mem_bytes = (size_t)s.npad * kMemSize;
+  const size_t n16 = mem_bytes / 16;
+  hipLaunchKernelGGL(fill_mem_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<uint4*>(s.mem), n16, s.boot);
+  hipLaunchKernelGGL(init_state_kernel, dim3((unsigned)((s.npad + 255) / 256)), dim3(256), 0, st,
+                     s.cs, s.sc, s.npad, s.mbc_kind);
+  return hipGetLastError();
+}
+
+hipError_t launch_render(const DevState& s, uint8_t* out, int64_t base, int packed,
+                         hipStream_t st) {
+  if (s.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(render_kernel, dim3((unsigned)((s.n + 255) / 256), kDsH), dim3(256), 0, st, s,
+                     out, base, packed);
+  return hipGetLastError();
+}
+
+hipError_t launch_snapshot(const DevState& s, const SnapState& snap, int env, int with_pix,
+                           hipStream_t st) {
+  hipLaunchKernelGGL(snapshot_kernel, dim3(kMemSize / 256 + ((s.cram_stride + 255) / 256) + 1),
+                     dim3(256), 0, st, s, snap, (uint32_t)env, with_pix);
+  return hipGetLastError();
+}
+
+hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const uint8_t* mask,
+                               hipStream_t st) {
+  if (s.n <= 0) return hipSuccess;
+  const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
+  const uint32_t chunks = (per_env + kResetChunk - 1) / kResetChunk;
+  hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + 255) / 256), chunks), dim3(256), 0,
+                     st, s, snap.mem, snap.cram, mask);
+  hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)s.n), dim3(256), 0, st, s, snap, mask,
+                     snap.has_pix);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const DevState& s, const uint16_t* addrs, int k, uint8_t* out,
+                         hipStream_t st) {
+  if (s.n <= 0 || k <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)((s.n + 255) / 256)), dim3(256), 0, st, s, addrs,
+                     k, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_hash(const DevState& s, const uint64_t* K, uint64_t* out, hipStream_t st) {
+  if (s.n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(hash_kernel, dim3((unsigned)((s.n + 255) / 256)), dim3(256), 0, st, s, K, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_export_mem(const DevState& s, int env_lo, int count, int lo, int len,
+                             uint8_t* dst, hipStream_t st) {
+  const size_t total = (size_t)count * (size_t)len;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(export_mem_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, s,
+                     (uint32_t)env_lo, (uint32_t)count, (uint32_t)lo, (uint32_t)len, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_import_mem(const DevState& s, int env, int addr, int len, const uint8_t* src,
+                             hipStream_t st) {
+  if (len <= 0) return hipSuccess;
+  hipLaunchKernelGGL(import_mem_kernel, dim3((unsigned)((len + 255) / 256)), dim3(256), 0, st, s,
+                     (uint32_t)env, (uint32_t)addr, (uint32_t)len, src);
+  return hipGetLastError();
+}
+
+hipError_t launch_export_cram(const DevState& s, int env_lo, int count, uint8_t* dst,
+                              hipStream_t st) {
+  const size_t total = (size_t)count * (size_t)s.cram_stride;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(export_cram_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, s,
+                     (uint32_t)env_lo, (uint32_t)count, dst);
+  return hipGetLastError();
+}
+
+}  // namespace gbx

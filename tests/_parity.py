@@ -1,0 +1,42 @@
+"""Comparison helpers: HIP backend state vs the oracle, field by field."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.ref import SCALAR_FIELDS
+
+
+def assert_same_state(dut, ref, *, step: int, tag: str, mem: bool = True) -> None:
+    """Every per-env scalar, the cart state, cart RAM, serial bytes and
+    (optionally) the full 64 KiB memory image must be identical."""
+    for name in SCALAR_FIELDS:
+        got = dut.export_field(name)
+        want = ref.field(name).astype(np.int64)
+        if not np.array_equal(got, want):
+            bad = np.nonzero(got != want)[0]
+            i = int(bad[0])
+            raise AssertionError(
+                f"[{tag} step {step}] field {name}: {len(bad)} envs differ; "
+                f"env {i}: hip={got[i]} oracle={want[i]} "
+                f"(pc hip={dut.export_field('pc')[i]:#x} oracle={ref.field('pc')[i]:#x})"
+            )
+    cs = dut.export_cart_state()
+    if not np.array_equal(cs, ref.cart_state):
+        bad = np.argwhere(cs != ref.cart_state)
+        raise AssertionError(f"[{tag} step {step}] cart_state differs at {bad[:5].tolist()}")
+    cr = dut.export_cart_ram()
+    if not np.array_equal(cr, ref.cart_ram):
+        bad = np.argwhere(cr != ref.cart_ram)
+        raise AssertionError(f"[{tag} step {step}] cart_ram differs at {bad[:5].tolist()}")
+    if not np.array_equal(dut.export_serial(), ref.serial_buf):
+        raise AssertionError(f"[{tag} step {step}] serial buffer differs")
+    if mem:
+        got = dut.export_memory()
+        if not np.array_equal(got, ref.mem):
+            bad = np.argwhere(got != ref.mem)
+            e, a = (int(x) for x in bad[0])
+            raise AssertionError(
+                f"[{tag} step {step}] memory differs in {len(bad)} bytes; first env {e} "
+                f"addr {a:#06x}: hip={got[e, a]:#04x} oracle={ref.mem[e, a]:#04x}"
+            )
