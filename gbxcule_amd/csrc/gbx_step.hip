@@ -671,7 +671,7 @@ struct Lane {
 // ---------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void step_kernel(DevState s, StepArgs args) {
+__global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (uint32_t)s.n) return;
   Lane L{s};
@@ -1203,7 +1203,9 @@ __global__ __launch_bounds__(256) void step_kernel(DevState s, StepArgs args) {
 
 hipError_t launch_step(const DevState& s, const StepArgs& a, hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
-  const int threads = 256;
+  // One wavefront per workgroup: small env counts (16K envs = 256 waves)
+  // spread over all CUs instead of packing 4 waves into a quarter of them.
+  const int threads = kEnvBlock;
   const int blocks = (s.n + threads - 1) / threads;
   hipLaunchKernelGGL(step_kernel, dim3(blocks), dim3(threads), 0, st, s, a);
   return hipGetLastError();
