@@ -184,6 +184,7 @@ def main() -> int:
     kernel_ms = float(np.mean(step_ms))
     value = n * steps / elapsed
     traps = int(be.export_field("trap_flag").sum())
+    lanes = be.step_lanes
     instr_gpu = float(be.export_field("instr_count").sum())
 
     # CPU baseline on a bounded prefix of the same trace; also yields the
@@ -238,6 +239,7 @@ def main() -> int:
             "render": wl.render,
             "reset_prob": wl.reset_prob,
             "senses": wl.senses,
+            "step_lanes": lanes,
         },
         "frames_per_sec": value * fs,
         "emulated_instr_per_sec": instr_gpu / max(warmup + steps, 1) / (elapsed / steps),

@@ -34,7 +34,8 @@ BUF_MEM, BUF_PIX, BUF_PIX_PACKED, BUF_OBS, BUF_REWARD, BUF_ACTIONS, BUF_CART_RAM
     INFO_MBC_KIND,
     INFO_OBS_DIM,
     INFO_CART_RAM_STRIDE,
-) = range(9)
+    INFO_STEP_LANES,
+) = range(10)
 
 # Every symbol the header declares, with its ctypes signature.
 _vp, _i32, _i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
@@ -82,6 +83,13 @@ def load() -> ctypes.CDLL:
                 f"{LIB_PATH} is missing: build it with gbxcule_amd.build.build() "
                 "(hipcc --offload-arch=gfx950)"
             )
+        # torch bundles its own HIP runtime under the same soname as ROCm's.
+        # Loading torch first makes the library bind to that runtime, so the
+        # process holds one HIP runtime and device pointers are shared with
+        # torch; loading the library first would put ROCm's runtime in place
+        # and torch would then find no GPU.
+        import torch  # noqa: F401
+
         lib = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

@@ -175,6 +175,11 @@ class HipVecBackend:
         self._call("gbx_buffer", self.ctx, which, ctypes.byref(ptr), ctypes.byref(nbytes))
         return int(ptr.value or 0), int(nbytes.value)
 
+    @property
+    def step_lanes(self) -> int:
+        """Envs per wavefront of the step kernel (64, 32, 16 or 8)."""
+        return self._info(_lib.INFO_STEP_LANES)
+
     def _info(self, key: int) -> int:
         out = ctypes.c_int64()
         self._call("gbx_info", self.ctx, key, ctypes.byref(out))

@@ -1,4 +1,5 @@
 // gbx_api.hip -- host implementation of the C ABI declared in include/gbx_hip.h.
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -6,6 +7,7 @@
 
 #include "../../include/gbx_hip.h"
 #include "gbx_aux.h"
+#include "gbx_decode.h"
 
 using namespace gbx;
 
@@ -50,7 +52,7 @@ constexpr int kHashLen = kMemSize + 128;
 void free_ctx(gbx_ctx* c) {
   DevState& s = c->s;
   void* ptrs[] = {s.mem, s.cram, s.cs, s.sc, s.cnt, s.serial, s.actions, s.obs, s.reward,
-                  s.pix, s.pix_packed, s.latches, (void*)s.rom, (void*)s.boot,
+                  s.pix, s.pix_packed, s.latches, (void*)s.rom, (void*)s.boot, (void*)s.recs,
                   c->snap.mem, c->snap.cram, c->snap.serial, c->snap.pix, c->snap.cs,
                   c->snap.sc, c->snap.cnt, c->hash_k};
   for (void* p : ptrs)
@@ -61,6 +63,26 @@ void free_ctx(gbx_ctx* c) {
 template <typename T>
 hipError_t dalloc(T** p, size_t count) {
   return hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T) > 0 ? count * sizeof(T) : 1);
+}
+
+// Pre-decoded instruction records for the step kernel's fetch: one 64-bit
+// word per ROM byte and per boot-image byte (after the ROM), holding the
+// opcode and the next two bytes of the same image in bits 0-23 and the
+// 40-bit micro-op decode (gbx_decode.h) in bits 24-63.  Bytes past the end
+// of an image read as 0; the kernel only uses a record when all three bytes
+// lie inside one 16 KiB ROM window or inside the boot image.
+std::vector<uint64_t> build_records(const uint8_t* rom, int64_t rom_bytes, const uint8_t* boot) {
+  std::vector<uint64_t> r((size_t)rom_bytes + 0x100);
+  auto fill = [&](const uint8_t* img, int64_t len, size_t base) {
+    for (int64_t i = 0; i < len; ++i) {
+      const uint32_t op = img[i], b1 = i + 1 < len ? img[i + 1] : 0u,
+                     b2 = i + 2 < len ? img[i + 2] : 0u;
+      r[base + (size_t)i] = (uint64_t)(op | (b1 << 8) | (b2 << 16)) | (decode_insn(op, b1) << 24);
+    }
+  };
+  fill(rom, rom_bytes, 0);
+  fill(boot, 0x100, (size_t)rom_bytes);
+  return r;
 }
 
 // Header parse (reference core/cartridge.py:139-187).
@@ -79,6 +101,28 @@ int parse_header(const uint8_t* rom, int64_t rom_len, int* kind, int64_t* rom_by
   *ram_bytes = ram_map[ramc];
   if (rom_len < *rom_bytes) return fail(GBX_E_INVALID, "ROM smaller than header advertises");
   return GBX_OK;
+}
+
+// Envs per step-kernel wavefront.  Each env is a serial instruction stream,
+// so a wavefront's time per emulated instruction is set by its dependent
+// memory round trips, not by how many lanes it carries.  Below ~4 wavefronts
+// per CU some SIMDs would sit idle, so small env counts are spread over
+// narrower workgroups (64 -> 32 -> 16 -> 8 envs) until every SIMD holds one.
+// GBX_STEP_LANES=64|32|16|8|4 overrides the choice (for tuning sweeps).
+int choose_step_lanes(int n) {
+  if (const char* v = getenv("GBX_STEP_LANES")) {
+    const int l = atoi(v);
+    if (l == 4 || l == 8 || l == 16 || l == 32 || l == 64) return l;
+  }
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int x = 0;
+    if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && x > 0)
+      cus = x;
+  }
+  int lanes = kEnvBlock;
+  while (lanes > 8 && (n + lanes - 1) / lanes < 4 * cus) lanes >>= 1;
+  return lanes;
 }
 
 }  // namespace
@@ -113,6 +157,7 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   s.cram_stride = ram_bytes > 0 ? ram_bytes : 1;
   s.mbc_kind = kind;
   s.rom_len = rom_bytes;
+  s.step_lanes = choose_step_lanes(num_envs);
   const size_t np = (size_t)s.npad;
   hipError_t e = hipSuccess;
   auto A = [&](hipError_t r) {
@@ -131,10 +176,13 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   A(dalloc(&s.pix_packed, (size_t)num_envs * kDsWB * kDsH));
   A(dalloc(&s.latches, (size_t)9 * kScreenH));
   uint8_t *drom = nullptr, *dboot = nullptr;
-  A(dalloc(&drom, (size_t)rom_bytes));
+  uint64_t* drecs = nullptr;
+  A(dalloc(&drom, (size_t)rom_bytes + 0x100));
   A(dalloc(&dboot, (size_t)0x100));
+  A(dalloc(&drecs, (size_t)rom_bytes + 0x100));
   s.rom = drom;
   s.boot = dboot;
+  s.recs = drecs;
   A(dalloc(&c->snap.mem, (size_t)kMemSize));
   A(dalloc(&c->snap.cram, (size_t)s.cram_stride));
   A(dalloc(&c->snap.serial, (size_t)kSerialMax));
@@ -149,8 +197,11 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   }
   std::vector<uint64_t> k(kHashLen);
   for (int i = 0; i < kHashLen; ++i) k[i] = splitmix((uint64_t)i);
+  const std::vector<uint64_t> recs = build_records(rom, rom_bytes, boot);
   A(hipMemcpy(drom, rom, (size_t)rom_bytes, hipMemcpyHostToDevice));
+  A(hipMemcpy(drom + rom_bytes, boot, 0x100, hipMemcpyHostToDevice));
   A(hipMemcpy(dboot, boot, 0x100, hipMemcpyHostToDevice));
+  A(hipMemcpy(drecs, recs.data(), recs.size() * sizeof(uint64_t), hipMemcpyHostToDevice));
   A(hipMemcpy(c->hash_k, k.data(), k.size() * 8, hipMemcpyHostToDevice));
   if (e != hipSuccess) {
     free_ctx(c);
@@ -443,6 +494,7 @@ int gbx_info(gbx_ctx* ctx, int32_t key, int64_t* out) {
     case GBX_INFO_MBC_KIND: *out = s.mbc_kind; break;
     case GBX_INFO_OBS_DIM: *out = s.obs_dim; break;
     case GBX_INFO_CART_RAM_STRIDE: *out = s.cram_stride; break;
+    case GBX_INFO_STEP_LANES: *out = s.step_lanes; break;
     default: return fail(GBX_E_INVALID, "unknown info key");
   }
   return GBX_OK;

@@ -66,7 +66,8 @@ enum {
 /* gbx_info keys. */
 enum { GBX_INFO_NUM_ENVS = 0, GBX_INFO_PADDED_ENVS, GBX_INFO_ROM_BANKS,
        GBX_INFO_ROM_BANK_MASK, GBX_INFO_RAM_BANKS, GBX_INFO_RAM_BYTES,
-       GBX_INFO_MBC_KIND, GBX_INFO_OBS_DIM, GBX_INFO_CART_RAM_STRIDE };
+       GBX_INFO_MBC_KIND, GBX_INFO_OBS_DIM, GBX_INFO_CART_RAM_STRIDE,
+       GBX_INFO_STEP_LANES };
 
 const char* gbx_last_error(void);
 int gbx_version(void);

@@ -24,7 +24,11 @@ def assert_same_state(dut, ref, *, step: int, tag: str, mem: bool = True) -> Non
     cs = dut.export_cart_state()
     if not np.array_equal(cs, ref.cart_state):
         bad = np.argwhere(cs != ref.cart_state)
-        raise AssertionError(f"[{tag} step {step}] cart_state differs at {bad[:5].tolist()}")
+        e = int(bad[0][0])
+        raise AssertionError(
+            f"[{tag} step {step}] cart_state differs in {len(bad)} slots, first at "
+            f"{bad[:5].tolist()}; env {e}: hip={cs[e].tolist()} oracle={ref.cart_state[e].tolist()}"
+        )
     cr = dut.export_cart_ram()
     if not np.array_equal(cr, ref.cart_ram):
         bad = np.argwhere(cr != ref.cart_ram)
