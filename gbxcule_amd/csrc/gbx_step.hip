@@ -103,12 +103,21 @@ struct Lane {
   // CPU: w0 = B C D E (B in bits 31-24), w1 = H L - A (A in bits 7-0)
   uint32_t pc, sp, f, w0, w1;
   uint32_t ime, ime_delay, halted;
-  // hot IO registers (byte values)
-  uint32_t ff04, tima, tma, tac, ifr, ie, lcdc, stat, lym, lyc, wy;
+  // hot IO registers (byte values); FF04 and the STAT mode/coincidence bits
+  // are derived from the timer and PPU position (ff04_val, stat_val)
+  uint32_t tima, tma, tac, ifr, ie, lcdc, lym, lyc, wy;
+  uint32_t stat_full;   // STAT as last written (low 3 bits valid while stat_fresh)
+  uint32_t stat_fresh;  // STAT written (or launch start) since the last PPU step
   // timer
-  uint32_t div, pend, delay, tprev;
+  uint32_t div, pend, delay;
+  uint32_t tmask;       // no TIMA edge while (div & tmask) + cycles <= tmask
+  uint32_t tp_w;        // DIV or TAC written this launch
+  uint32_t ff04_0, tprev0;  // FF04 and timer_prev_in as loaded
   // PPU
-  uint32_t scan, ly, wl, stat_prev;
+  uint32_t scan, ly, wl;
+  uint32_t sp0;         // ppu_stat_prev as loaded (until the first PPU step)
+  uint32_t lyc_pp;      // LYC at the last PPU step
+  uint32_t lcd_pp;      // LCDC bit 7 at the last PPU step; 0x100 before the first
   // cartridge
   uint32_t boot_en;
   int rom_lo, rom_hi;  // byte offset of the 0000 / 4000 windows, -1 = open bus
@@ -190,13 +199,13 @@ struct Lane {
   // Hot IO registers live in VGPRs; every other FFxx byte is in memory.
   __device__ uint32_t io_hot(uint32_t x, uint32_t v) const {
     const uint32_t k = x & 0xFFu;
-    v = sel(k == 0x04u, ff04, v);
+    v = sel(k == 0x04u, ff04_val(), v);
     v = sel(k == 0x05u, tima, v);
     v = sel(k == 0x06u, tma, v);
     v = sel(k == 0x07u, tac, v);
     v = sel(k == 0x0Fu, ifr, v);
     v = sel(k == 0x40u, lcdc, v);
-    v = sel(k == 0x41u, stat, v);
+    v = sel(k == 0x41u, stat_val(), v);
     v = sel(k == 0x44u, lym, v);
     v = sel(k == 0x45u, lyc, v);
     v = sel(k == 0x4Au, wy, v);
@@ -264,11 +273,19 @@ struct Lane {
     pend = 0;
     delay = 0;
   }
+  __device__ static uint32_t edge_mask(uint32_t t) {
+    return (t & 4u) ? (2u << div_bit(t)) - 1u : 0x7FFFFFFFu;
+  }
+  // FF04 and timer_prev_in as the reference holds them: derived from the DIV
+  // counter once it has ticked or been written this launch.
+  __device__ bool timer_live() const { return lcd_pp != 0x100u || tp_w != 0u; }
+  __device__ uint32_t ff04_val() const { return timer_live() ? (div >> 8) & 0xFFu : ff04_0; }
+  __device__ uint32_t tprev_val() const { return timer_live() ? timer_in(div, tac) : tprev0; }
   __device__ void timer_tick(int cycles) {
     if (cycles <= 0) return;
     uint32_t d = div & 0xFFFFu;
-    if (!(tac & 4u) && !pend) {
-      d = (d + (uint32_t)cycles) & 0xFFFFu;  // no edges, no reload: DIV only
+    if (!pend && (d & tmask) + (uint32_t)cycles <= tmask) {
+      d = (d + (uint32_t)cycles) & 0xFFFFu;  // no edge, no reload: DIV only
     } else {
       int rem = cycles;
       while (rem > 0) {
@@ -290,8 +307,6 @@ struct Lane {
       }
     }
     div = d;
-    ff04 = (d >> 8) & 0xFFu;
-    tprev = timer_in(d, tac);
   }
 
   // -- MBC3 real-time clock (cpu_step_builder.py:374-419) ----------------------
@@ -364,7 +379,8 @@ struct Lane {
     ifr = sel(k == 0x0Fu, v & 0x1Fu, ifr);
     ie = sel(k == 0xFFu, v & 0x1Fu, ie);
     lcdc = sel(k == 0x40u, v, lcdc);
-    stat = sel(k == 0x41u, v, stat);
+    stat_fresh = sel(k == 0x41u, 1u, stat_fresh);
+    stat_full = sel(k == 0x41u, v, stat_full);
     lym = sel(k == 0x44u, v, lym);
     lyc = sel(k == 0x45u, v, lyc);
     wy = sel(k == 0x4Au, v, wy);
@@ -398,18 +414,16 @@ struct Lane {
         break;
       case 0x04: {
         const uint32_t pre = timer_in(div, tac);
-        ff04 = 0;
         div = 0;
-        const uint32_t post = timer_in(0, tac);
-        tprev = post;
-        if (pre && !post) tima_inc();
+        tp_w = 1;
+        if (pre && !timer_in(0, tac)) tima_inc();
       } break;
       case 0x07: {
         const uint32_t pre = timer_in(div, tac);
         tac = v & 7u;
-        const uint32_t post = timer_in(div, tac);
-        tprev = post;
-        if (pre && !post) tima_inc();
+        tmask = edge_mask(tac);
+        tp_w = 1;
+        if (pre && !timer_in(div, tac)) tima_inc();
       } break;
       case 0x46: {
         M(0xFF46) = v;
@@ -495,6 +509,53 @@ struct Lane {
     Lt[7 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF48);
     Lt[8 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF49);
   }
+  // STAT mode of the current position (LCD on)
+  __device__ uint32_t mode_now(uint32_t sc) const {
+    return ly >= (uint32_t)kScreenH ? 1u : sc < 80u ? 2u : sc < 250u ? 3u : 0u;
+  }
+  __device__ static uint32_t stat_bits(uint32_t mode, uint32_t coin) {
+    return (mode == 0 ? 1u : 0u) | (mode == 1 ? 2u : 0u) | (mode == 2 ? 4u : 0u) | (coin << 3);
+  }
+  // STAT as the reference holds it: every PPU step rewrites the low three
+  // bits (coincidence, mode) from the position it ends at, so they are
+  // derived here from that position instead of being stored per step.
+  __device__ uint32_t stat_val() const {
+    if (stat_fresh) return stat_full;
+    const uint32_t coin = ly == lyc_pp ? 1u : 0u;
+    return (stat_full & 0xF8u) | (coin << 2) | (lcd_pp ? mode_now(scan) : 0u);
+  }
+  // ppu_stat_prev as the reference holds it after the last PPU step that
+  // ended at scanline cycle sc.
+  __device__ uint32_t stat_prev_at(uint32_t sc) const {
+    if (lcd_pp == 0x100u) return sp0;
+    if (!lcd_pp) return 0u;
+    return stat_bits(mode_now(sc), ly == lyc_pp ? 1u : 0u);
+  }
+  // Line change(s) after scan reached 456; s0 = scanline cycle before the step.
+  __device__ void ppu_lines(uint32_t s0) {
+    uint32_t prev = stat_prev_at(s0);
+    const uint32_t lc = lcdc;
+    uint32_t total = scan;
+    while (total >= (uint32_t)kCyclesPerLine) {
+      total -= kCyclesPerLine;
+      const uint32_t pl = ly;
+      if (pl < (uint32_t)kScreenH && (lc & 0x20u) && pl >= wy) wl += 1;
+      ly = (ly + 1u) % (uint32_t)kLinesPerFrame;
+      if (ly == 0) wl = 0;
+      lym = ly;
+      // ppu_update_stat_irq with mode 0 or 1
+      const uint32_t mode = ly >= (uint32_t)kScreenH ? 1u : 0u;
+      const uint32_t coin = ly == lyc ? 1u : 0u;
+      const uint32_t cur = (mode == 0 ? 1u : 0u) | (mode == 1 ? 2u : 0u) | (coin << 3);
+      const uint32_t en = (stat_full >> 3) & 0xFu;  // bit0 mode0, 1 mode1, 2 mode2, 3 lyc
+      if (en & cur & ~(prev & 0xFu)) ifr |= 0x02u;
+      prev = cur;
+      if (pl == 143u && ly == 144u) ifr |= 0x01u;
+      if (ly < (uint32_t)kScreenH) latch_env0();
+    }
+    scan = total;
+  }
+  // One PPU step of `cycles` (cycles > 0).
   __device__ uint32_t ppu_advance(int cycles) {
     const uint32_t lc = lcdc;
     if (!(lc & 0x80u)) {
@@ -502,40 +563,14 @@ struct Lane {
       ly = 0;
       wl = 0;
       lym = 0;
-      stat = (stat & 0xF8u) | ((lyc == 0u) ? 4u : 0u);
-      stat_prev = 0;
-      return lc;
+    } else {
+      const uint32_t s0 = scan;
+      scan = s0 + (uint32_t)cycles;
+      if (scan >= (uint32_t)kCyclesPerLine) ppu_lines(s0);
     }
-    int total = (int)scan + cycles;
-    int lines = 0;
-    while (total >= kCyclesPerLine) {
-      total -= kCyclesPerLine;
-      ++lines;
-    }
-    scan = (uint32_t)total;
-    if (lines == 0 && scan == 0) latch_env0();
-    for (; lines > 0; --lines) {
-      const uint32_t prev = ly;
-      if (prev < (uint32_t)kScreenH && (lc & 0x20u) && prev >= wy) wl += 1;
-      ly = (ly + 1u) % (uint32_t)kLinesPerFrame;
-      if (ly == 0) wl = 0;
-      lym = ly;
-      // ppu_update_stat_irq with mode 0 or 1
-      const uint32_t mode = ly >= (uint32_t)kScreenH ? 1u : 0u;
-      const uint32_t coin = ly == lyc ? 1u : 0u;
-      const uint32_t keep = stat & 0xF8u;
-      stat = keep | (coin << 2) | mode;
-      const uint32_t cur = (mode == 0 ? 1u : 0u) | (mode == 1 ? 2u : 0u) | (coin << 3);
-      const uint32_t en = (keep >> 3) & 0xFu;  // bit0 mode0, bit1 mode1, bit2 mode2, bit3 lyc
-      if (en & cur & ~(stat_prev & 0xFu)) ifr |= 0x02u;
-      stat_prev = cur;
-      if (prev == 143u && ly == 144u) ifr |= 0x01u;
-      if (ly < (uint32_t)kScreenH) latch_env0();
-    }
-    const uint32_t mode = ly >= (uint32_t)kScreenH ? 1u : scan < 80u ? 2u : scan < 250u ? 3u : 0u;
-    const uint32_t coin = ly == lyc ? 1u : 0u;
-    stat = (stat & 0xF8u) | (coin << 2) | mode;
-    stat_prev = (mode == 0 ? 1u : 0u) | (mode == 1 ? 2u : 0u) | (mode == 2 ? 4u : 0u) | (coin << 3);
+    stat_fresh = 0;
+    lyc_pp = lyc;
+    lcd_pp = lc & 0x80u;
     return lc;
   }
 
@@ -620,20 +655,25 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   L.ime_delay = (uint32_t)L.SC(F_IME_DELAY);
   L.halted = (uint32_t)L.SC(F_HALTED);
   L.div = (uint32_t)L.SC(F_DIV_COUNTER);
-  L.tprev = (uint32_t)L.SC(F_TIMER_PREV_IN);
+  L.tprev0 = (uint32_t)L.SC(F_TIMER_PREV_IN);
   L.pend = (uint32_t)L.SC(F_TIMA_PENDING);
   L.delay = (uint32_t)L.SC(F_TIMA_DELAY);
   L.scan = (uint32_t)L.SC(F_PPU_SCANLINE);
   L.ly = (uint32_t)L.SC(F_PPU_LY);
   L.wl = (uint32_t)L.SC(F_PPU_WINDOW_LINE);
-  L.stat_prev = (uint32_t)L.SC(F_PPU_STAT_PREV);
-  L.ff04 = L.M(0xFF04);
+  L.sp0 = (uint32_t)L.SC(F_PPU_STAT_PREV);
+  L.ff04_0 = L.M(0xFF04);
   L.tima = L.M(0xFF05);
   L.tma = L.M(0xFF06);
   L.tac = L.M(0xFF07);
+  L.tmask = Lane::edge_mask(L.tac);
   L.ifr = L.M(0xFF0F);
   L.lcdc = L.M(0xFF40);
-  L.stat = L.M(0xFF41);
+  L.stat_full = L.M(0xFF41);
+  L.stat_fresh = 1;
+  L.lyc_pp = 0;
+  L.lcd_pp = 0x100u;
+  L.tp_w = 0;
   L.lym = L.M(0xFF44);
   L.lyc = L.M(0xFF45);
   L.wy = L.M(0xFF4A);
@@ -661,6 +701,8 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   int64_t instr = ld64(0);
   const int64_t instr_start = instr;
   int64_t cyc = ld64(1);
+  // per-launch increments, folded into the 64-bit counters at frame ends
+  uint32_t ninstr = 0, ncyc = 0;
   int cframe = L.SC(F_CYCLE_IN_FRAME);
   int trap = L.SC(F_TRAP_FLAG), trap_pc = L.SC(F_TRAP_PC);
   int trap_op = L.SC(F_TRAP_OPCODE), trap_kind = L.SC(F_TRAP_KIND);
@@ -671,6 +713,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   };
   const uint32_t watch_val = dbg_watch ? watch_read() : 0u;
   const int frames = args.frames;
+  const bool dbg = args.dbg_rst38 || args.dbg_trap_pc || args.dbg_max_instr > 0 || dbg_watch;
 
   // record of the instruction at pc (valid when rv)
   uint32_t rlo = 0, rhi = 0;
@@ -701,13 +744,15 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       }
       op = rlo & 0xFFu;
       const uint32_t b1 = (rlo >> 8) & 0xFFu, b2 = (rlo >> 16) & 0xFFu;
-      if (args.dbg_trap_pc && pc == (uint32_t)args.dbg_trap_pc) {
-        if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5; }
-        break;
-      }
-      if (args.dbg_rst38 && op == 0xFFu && pc != 0x0038u) {
-        if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 3; }
-        break;
+      if (dbg) {
+        if (args.dbg_trap_pc && pc == (uint32_t)args.dbg_trap_pc) {
+          if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5; }
+          break;
+        }
+        if (args.dbg_rst38 && op == 0xFFu && pc != 0x0038u) {
+          if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 3; }
+          break;
+        }
       }
       const uint32_t len = (rlo >> 24) & 3u, cyc4 = (rlo >> 26) & 7u, cycnt4 = rlo >> 29;
       const uint32_t am = rhi & 7u, nr = (rhi >> 3) & 3u, hlinc = (rhi >> 5) & 3u;
@@ -904,7 +949,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       int tcyc = 20;
       if (pass == 0) {
         if (!hiter) {
-          if (args.dbg_rst38 && L.pc >= 0xFE00u) {
+          if (dbg && args.dbg_rst38 && L.pc >= 0xFE00u) {
             if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4; }
             stop = true;
             break;
@@ -913,16 +958,18 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
             stop = true;
             break;
           }
-          instr += 1;
-          if (args.dbg_max_instr > 0 && instr - instr_start >= args.dbg_max_instr) {
-            if (!trap) { trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6; }
-            stop = true;
-            break;
-          }
-          if (dbg_watch && watch_read() != watch_val) {
-            if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 7; }
-            stop = true;
-            break;
+          ninstr += 1;
+          if (dbg) {
+            if (args.dbg_max_instr > 0 && instr + ninstr - instr_start >= args.dbg_max_instr) {
+              if (!trap) { trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6; }
+              stop = true;
+              break;
+            }
+            if (dbg_watch && watch_read() != watch_val) {
+              if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 7; }
+              stop = true;
+              break;
+            }
           }
         }
         tcyc = cycles;
@@ -967,8 +1014,14 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
 
     const int total = cycles + svc;
     L.rtc_tick(total);
-    cyc += total;
+    ncyc += (uint32_t)total;
     cframe += total;
+    if (!(((lcdc_prev ^ lcdc_now) & 0x80u) || cframe >= kCyclesPerFrame)) continue;
+    // LCD toggles and frame ends (cpu_step_builder.py frame loop)
+    instr += ninstr;
+    cyc += ncyc;
+    ninstr = 0;
+    ncyc = 0;
     if (lcdc_prev && !(lcdc_now & 0x80u)) {
       int tail = 0;
       if (!hiter) {
@@ -987,9 +1040,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       L.ly = 0;
       L.wl = 0;
       L.lym = 0;
-      const uint32_t coin = L.lyc == 0 ? 1u : 0u;
-      L.stat = (L.stat & 0xF8u) | (coin << 2) | 2u;
-      L.stat_prev = 4u | (coin << 3);
+      L.stat_fresh = 0;  // STAT and stat_prev follow from scan 0 of line 0
       cframe = 0;
       if (++L.frames_done >= frames) break;
       continue;
@@ -999,6 +1050,8 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       if (++L.frames_done >= frames) break;
     }
   }
+  instr += ninstr;
+  cyc += ncyc;
 
   // ---- post-step outputs (cpu_templates/post_step.py) ----------------------
   const int stage = args.stage;
@@ -1057,20 +1110,20 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   L.SC(F_IME_DELAY) = (int32_t)L.ime_delay;
   L.SC(F_HALTED) = (int32_t)L.halted;
   L.SC(F_DIV_COUNTER) = (int32_t)L.div;
-  L.SC(F_TIMER_PREV_IN) = (int32_t)L.tprev;
+  L.SC(F_TIMER_PREV_IN) = (int32_t)L.tprev_val();
   L.SC(F_TIMA_PENDING) = (int32_t)L.pend;
   L.SC(F_TIMA_DELAY) = (int32_t)L.delay;
   L.SC(F_PPU_SCANLINE) = (int32_t)L.scan;
   L.SC(F_PPU_LY) = (int32_t)L.ly;
   L.SC(F_PPU_WINDOW_LINE) = (int32_t)L.wl;
-  L.SC(F_PPU_STAT_PREV) = (int32_t)L.stat_prev;
-  L.M(0xFF04) = L.ff04;
+  L.SC(F_PPU_STAT_PREV) = (int32_t)L.stat_prev_at(L.scan);
+  L.M(0xFF04) = L.ff04_val();
   L.M(0xFF05) = L.tima;
   L.M(0xFF06) = L.tma;
   L.M(0xFF07) = L.tac;
   L.M(0xFF0F) = L.ifr;
   L.M(0xFF40) = L.lcdc;
-  L.M(0xFF41) = L.stat;
+  L.M(0xFF41) = L.stat_val();
   L.M(0xFF44) = L.lym;
   L.M(0xFF45) = L.lyc;
   L.M(0xFF4A) = L.wy;
