@@ -210,10 +210,23 @@ def main() -> int:
     bytes_per_env_step = STATE_BYTES + data_b
     achieved = n * bytes_per_env_step / (kernel_ms * 1e-3) / 1e9
     traffic = None
-    tfile = ROOT / "profiles" / f"traffic_{args.workload}.json"
-    if tfile.exists() and not (args.envs or args.frameskip):
+    valu = None
+    tfile = ROOT / "profiles" / f"traffic_{args.workload}_{n}.json"
+    if tfile.exists() and fs == WORKLOADS[args.workload].frames_per_step:
         t = json.loads(tfile.read_text())
         traffic = t.get("bytes_per_launch")
+        if t.get("valu_wave_insts_per_launch"):
+            # VALU issue slots: profiled wave-instructions per launch x 64 lanes
+            # over this run's measured kernel time
+            lane_ops = t["valu_wave_insts_per_launch"] * 64 / (kernel_ms * 1e-3)
+            peak = t["valu_peak_lane_ops_per_s"]
+            valu = {
+                "achieved": lane_ops,
+                "peak": peak,
+                "unit": "lane-op/s",
+                "frac": lane_ops / peak,
+                "source": t.get("source"),
+            }
     out = {
         "metric": METRIC,
         "value": value,
@@ -256,6 +269,7 @@ def main() -> int:
             "bytes_per_env_step": bytes_per_env_step,
             "instr_per_env_step": instr_b,
         },
+        "valu": valu,
         "cpu_baseline": cpu,
     }
     be.close()
