@@ -65,6 +65,10 @@ hipError_t dalloc(T** p, size_t count) {
   return hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T) > 0 ? count * sizeof(T) : 1);
 }
 
+// The ROM buffer is the ROM, then the boot image, then one 16 KiB window of
+// 0xFF that an unmapped ROM bank reads (open bus).
+constexpr int64_t kOpenBusBytes = 0x4000;
+
 // Pre-decoded instruction records for the step kernel's fetch: one 64-bit
 // word per ROM byte and per boot-image byte (after the ROM), holding the
 // opcode and the next two bytes of the same image in bits 0-23 and the
@@ -72,7 +76,7 @@ hipError_t dalloc(T** p, size_t count) {
 // of an image read as 0; the kernel only uses a record when all three bytes
 // lie inside one 16 KiB ROM window or inside the boot image.
 std::vector<uint64_t> build_records(const uint8_t* rom, int64_t rom_bytes, const uint8_t* boot) {
-  std::vector<uint64_t> r((size_t)rom_bytes + 0x100);
+  std::vector<uint64_t> r((size_t)rom_bytes + 0x100 + kOpenBusBytes);
   auto fill = [&](const uint8_t* img, int64_t len, size_t base) {
     for (int64_t i = 0; i < len; ++i) {
       const uint32_t op = img[i], b1 = i + 1 < len ? img[i + 1] : 0u,
@@ -82,6 +86,8 @@ std::vector<uint64_t> build_records(const uint8_t* rom, int64_t rom_bytes, const
   };
   fill(rom, rom_bytes, 0);
   fill(boot, 0x100, (size_t)rom_bytes);
+  const std::vector<uint8_t> ff(kOpenBusBytes, 0xFF);
+  fill(ff.data(), kOpenBusBytes, (size_t)rom_bytes + 0x100);
   return r;
 }
 
@@ -177,9 +183,9 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   A(dalloc(&s.latches, (size_t)9 * kScreenH));
   uint8_t *drom = nullptr, *dboot = nullptr;
   uint64_t* drecs = nullptr;
-  A(dalloc(&drom, (size_t)rom_bytes + 0x100));
+  A(dalloc(&drom, (size_t)(rom_bytes + 0x100 + kOpenBusBytes)));
   A(dalloc(&dboot, (size_t)0x100));
-  A(dalloc(&drecs, (size_t)rom_bytes + 0x100));
+  A(dalloc(&drecs, (size_t)(rom_bytes + 0x100 + kOpenBusBytes)));
   s.rom = drom;
   s.boot = dboot;
   s.recs = drecs;
@@ -200,6 +206,7 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   const std::vector<uint64_t> recs = build_records(rom, rom_bytes, boot);
   A(hipMemcpy(drom, rom, (size_t)rom_bytes, hipMemcpyHostToDevice));
   A(hipMemcpy(drom + rom_bytes, boot, 0x100, hipMemcpyHostToDevice));
+  A(hipMemset(drom + rom_bytes + 0x100, 0xFF, (size_t)kOpenBusBytes));
   A(hipMemcpy(dboot, boot, 0x100, hipMemcpyHostToDevice));
   A(hipMemcpy(drecs, recs.data(), recs.size() * sizeof(uint64_t), hipMemcpyHostToDevice));
   A(hipMemcpy(c->hash_k, k.data(), k.size() * 8, hipMemcpyHostToDevice));

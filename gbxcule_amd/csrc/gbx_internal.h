@@ -80,9 +80,9 @@ struct DevState {
   uint8_t* pix;         // [n][72][80]
   uint8_t* pix_packed;  // [n][72][20]
   uint8_t* latches;     // [9][144] env-0 scanline latches
-  const uint8_t* rom;       // ROM image, followed by the 256-byte boot image
+  const uint8_t* rom;       // ROM image, the 256-byte boot image, 16 KiB of 0xFF (open bus)
   const uint8_t* boot;
-  const uint64_t* recs;     // pre-decoded instruction per ROM byte, then per boot byte
+  const uint64_t* recs;     // pre-decoded instruction per byte of the ROM buffer
   int n, npad, obs_dim;
   int rom_banks, rom_mask, ram_banks, ram_bytes, cram_stride, mbc_kind;
   int step_lanes;       // envs per step-kernel wavefront: 64, 32, 16 or 8

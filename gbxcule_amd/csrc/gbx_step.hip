@@ -89,6 +89,21 @@ struct Ref32 {
 
 __device__ __forceinline__ uint32_t sel(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
 
+// Launch-uniform values that the loop only uses in per-lane arithmetic (flat
+// base addresses, sizes, limits) are held in VGPRs: the loop body already
+// keeps SGPRs busy with buffer descriptors and nested exec masks, and an
+// SGPR-held copy would be spilled and reloaded every iteration.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "r"(v));
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ T* in_vgpr(T* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return reinterpret_cast<T*>(((uint64_t)in_vgpr((uint32_t)(a >> 32)) << 32) | in_vgpr((uint32_t)a));
+}
+
 // ---------------------------------------------------------------------------
 // Per-lane machine.  Everything here is scalarized into VGPRs.
 // ---------------------------------------------------------------------------
@@ -99,6 +114,8 @@ struct Lane {
   rsrc_t rm, rsc, rcs;             // memory image, scalars, cartridge state of the block
   const uint8_t* memb;             // memory image of the block (flat)
   const uint8_t* cramb;            // cartridge RAM of the block (flat)
+  const uint8_t* rom;              // ROM buffer (flat)
+  uint32_t rom_len;
 
   // CPU: w0 = B C D E (B in bits 31-24), w1 = H L - A (A in bits 7-0)
   uint32_t pc, sp, f, w0, w1;
@@ -120,7 +137,7 @@ struct Lane {
   uint32_t lcd_pp;      // LCDC bit 7 at the last PPU step; 0x100 before the first
   // cartridge
   uint32_t boot_en;
-  int rom_lo, rom_hi;  // byte offset of the 0000 / 4000 windows, -1 = open bus
+  uint32_t rom_lo, rom_hi;  // byte offset of the 0000 / 4000 windows in the ROM buffer
   uint32_t ram_ok, ram_off;
   int rtc_field;       // 0..4 when an RTC register is mapped at A000
   int rtc_sub;
@@ -177,8 +194,10 @@ struct Lane {
     b0 = clamp_bank(b0, s.rom_banks, s.rom_mask);
     b1 = clamp_bank(b1, s.rom_banks, s.rom_mask);
     const int64_t lim = (int64_t)s.rom_banks * 0x4000;
-    rom_lo = ((int64_t)b0 * 0x4000 < lim) ? b0 * 0x4000 : -1;
-    rom_hi = ((int64_t)b1 * 0x4000 < lim) ? b1 * 0x4000 : -1;
+    // an unmapped bank reads the 0xFF filler that follows the boot image
+    const uint32_t open = rom_len + 0x100u;
+    rom_lo = ((int64_t)b0 * 0x4000 < lim) ? (uint32_t)b0 * 0x4000u : open;
+    rom_hi = ((int64_t)b1 * 0x4000 < lim) ? (uint32_t)b1 * 0x4000u : open;
     ram_ok = (s.ram_banks > 0 && CS(CS_RAM_ENABLE) != 0) ? 1u : 0u;
     rtc_field = -1;
     if (kind == MBC_MBC3) {
@@ -196,37 +215,28 @@ struct Lane {
   }
 
   // -- bus read (reference read8, cpu_step_builder.py:538-657) ----------------
-  // Hot IO registers live in VGPRs; every other FFxx byte is in memory.
-  __device__ uint32_t io_hot(uint32_t x, uint32_t v) const {
-    const uint32_t k = x & 0xFFu;
-    v = sel(k == 0x04u, ff04_val(), v);
-    v = sel(k == 0x05u, tima, v);
-    v = sel(k == 0x06u, tma, v);
-    v = sel(k == 0x07u, tac, v);
-    v = sel(k == 0x0Fu, ifr, v);
-    v = sel(k == 0x40u, lcdc, v);
-    v = sel(k == 0x41u, stat_val(), v);
-    v = sel(k == 0x44u, lym, v);
-    v = sel(k == 0x45u, lyc, v);
-    v = sel(k == 0x4Au, wy, v);
-    v = sel(k == 0xFFu, ie, v);
-    return v;
+  // Every IO register the core keeps in a VGPR is also stored to memory when
+  // it changes, so the bus reads memory for all of FF00-FFFF except FF04 and
+  // the STAT mode/coincidence bits, which follow from the DIV counter and the
+  // PPU position.
+  __device__ uint32_t io_fix(uint32_t x, uint32_t v) const {
+    v = x == 0xFF04u ? ff04_val() : v;
+    return x == 0xFF41u ? stat_val() : v;
   }
-  // Flat address of the byte the bus returns at x (echo-folded), for every
-  // source but the RTC registers and the hot IO registers.  *open is set
-  // when the bus returns 0xFF instead (unmapped ROM bank, disabled RAM).
-  __device__ const uint8_t* bus_ptr(uint32_t x, bool* open) const {
+  __device__ static bool io_derived(uint32_t x) { return (x & 0xFFBAu) == 0xFF00u; }
+  // Flat address of the byte the bus returns at x (echo-folded): ROM window,
+  // boot image, or the 0xFF filler for an unmapped bank; cartridge RAM; or
+  // the env's memory.  Disabled cartridge RAM and the RTC registers are
+  // resolved by cart_fix.
+  __device__ const uint8_t* bus_ptr(uint32_t x) const {
     const bool rom = x < 0x8000u;
     const bool cart = x - 0xA000u < 0x2000u;
-    const bool boot = boot_en && x < 0x100u;
-    const int win = x < 0x4000u ? rom_lo : rom_hi;
-    const uint32_t roff =
-        boot ? (uint32_t)s.rom_len + x : (uint32_t)(win < 0 ? 0 : win) + (x & 0x3FFFu);
+    const uint32_t roff = (boot_en && x < 0x100u) ? rom_len + x
+                                                   : (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
     const uint32_t coff = ram_ok ? ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane : lane;
-    *open = (rom && !boot && win < 0) || (cart && !ram_ok);
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
     p = cart ? cramb + coff : p;
-    p = rom ? s.rom + roff : p;
+    p = rom ? this->rom + roff : p;
     return p;
   }
   __device__ static uint32_t fold(uint32_t addr) {
@@ -237,18 +247,23 @@ struct Lane {
     const bool latched = CS(CS_RTC_LATCH) != 0;
     return (uint32_t)CS((latched ? CS_RTC_L_SECONDS : CS_RTC_SECONDS) + rtc_field) & 0xFFu;
   }
+  __device__ uint32_t cart_fix(uint32_t v) const {
+    if (!ram_ok) return 0xFFu;
+    return rtc_field >= 0 ? rtc_read() : v;
+  }
   // Value the bus returned for a load v issued at bus_ptr(x).
-  __device__ uint32_t bus_fix(uint32_t x, uint32_t v, bool open) const {
-    v = open ? 0xFFu : v;
-    if (x >= 0xFF00u) v = io_hot(x, v);
-    if (x - 0xA000u < 0x2000u && ram_ok && rtc_field >= 0) v = rtc_read();
+  __device__ uint32_t bus_fix(uint32_t x, uint32_t v) const {
+    if (x - 0xA000u < 0x2000u) v = cart_fix(v);
+    if (io_derived(x)) v = io_fix(x, v);
     return v;
   }
   __device__ uint32_t read8(uint32_t addr) const {
     const uint32_t x = fold(addr);
-    bool open;
-    const uint8_t* p = bus_ptr(x, &open);
-    return bus_fix(x, *p, open);
+    return bus_fix(x, *bus_ptr(x));
+  }
+  __device__ void set_if(uint32_t v) {
+    ifr = v;
+    M(0xFF0F) = v;
   }
 
   // -- timer (cpu_step_builder.py:249-372) -------------------------------------
@@ -305,6 +320,8 @@ struct Lane {
         if (edge) tima_inc();
         if (pend && (int)delay <= 0) reload_now();
       }
+      M(0xFF05) = tima;
+      M(0xFF0F) = ifr;
     }
     div = d;
   }
@@ -384,6 +401,14 @@ struct Lane {
     lym = sel(k == 0x44u, v, lym);
     lyc = sel(k == 0x45u, v, lyc);
     wy = sel(k == 0x4Au, v, wy);
+    // memory keeps the value the register holds after the write
+    uint32_t mv = v;
+    mv = sel(k == 0x0Fu, ifr, mv);
+    mv = sel(k == 0xFFu, ie, mv);
+    mv = sel(k == 0x07u, v & 7u, mv);
+    if (k - 0x05u < 3u || k == 0x0Fu || k == 0x40u || k == 0x44u || k == 0x45u || k == 0x4Au ||
+        k == 0xFFu)
+      M(x) = mv;
     switch (k) {
       case 0x00: {
         const uint32_t sl = v & 0x30u;
@@ -400,7 +425,7 @@ struct Lane {
             SC(F_SERIAL_OVERFLOW) = 1;
           }
           M(0xFF02) = v & 0x7Fu;
-          ifr |= 0x08u;
+          set_if(ifr | 0x08u);
         } else {
           M(0xFF02) = v;
         }
@@ -417,6 +442,7 @@ struct Lane {
         div = 0;
         tp_w = 1;
         if (pre && !timer_in(0, tac)) tima_inc();
+        M(0xFF05) = tima;
       } break;
       case 0x07: {
         const uint32_t pre = timer_in(div, tac);
@@ -424,6 +450,7 @@ struct Lane {
         tmask = edge_mask(tac);
         tp_w = 1;
         if (pre && !timer_in(div, tac)) tima_inc();
+        M(0xFF05) = tima;
       } break;
       case 0x46: {
         M(0xFF46) = v;
@@ -432,7 +459,7 @@ struct Lane {
         for (uint32_t j = 0; j < 160; ++j) {
           const uint32_t sa = (src + j) & 0xFFFFu;
           const uint32_t b = M(sa);
-          M(0xFE00u + j) = sa >= 0xFF00u ? io_hot(sa, b) : b;
+          M(0xFE00u + j) = io_derived(sa) ? io_fix(sa, b) : b;
         }
       } break;
       default:
@@ -554,6 +581,8 @@ struct Lane {
       if (ly < (uint32_t)kScreenH) latch_env0();
     }
     scan = total;
+    M(0xFF44) = lym;
+    M(0xFF0F) = ifr;
   }
   // One PPU step of `cycles` (cycles > 0).
   __device__ uint32_t ppu_advance(int cycles) {
@@ -562,7 +591,10 @@ struct Lane {
       scan = 0;
       ly = 0;
       wl = 0;
-      lym = 0;
+      if (lym) {
+        lym = 0;
+        M(0xFF44) = 0u;
+      }
     } else {
       const uint32_t s0 = scan;
       scan = s0 + (uint32_t)cycles;
@@ -607,13 +639,11 @@ struct Lane {
   // one 16 KiB ROM window of a mapped bank, or in the boot image.
   __device__ bool rec_ok(uint32_t p) const {
     if (boot_en && p < 0x100u) return p < 0xFEu;
-    const int win = p < 0x4000u ? rom_lo : rom_hi;
-    return p < 0x8000u && (p & 0x3FFFu) <= 0x3FFDu && win >= 0;
+    return p < 0x8000u && (p & 0x3FFFu) <= 0x3FFDu;
   }
   __device__ uint32_t rec_index(uint32_t p) const {
-    const int win = p < 0x4000u ? rom_lo : rom_hi;
-    return (boot_en && p < 0x100u) ? (uint32_t)s.rom_len + p
-                                   : (uint32_t)(win < 0 ? 0 : win) + (p & 0x3FFFu);
+    return (boot_en && p < 0x100u) ? rom_len + p
+                                   : (p < 0x4000u ? rom_lo : rom_hi) + (p & 0x3FFFu);
   }
   // Fetch + decode through the bus (code in RAM, window edges, open bus).
   __device__ void fetch_slow(uint32_t& rlo, uint32_t& rhi) const {
@@ -634,14 +664,16 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   L.e = e;
   L.lane = e & (kEnvBlock - 1);
   const uint32_t blk = __builtin_amdgcn_readfirstlane(e >> kEnvBlockShift);
-  L.memb = s.mem + ((size_t)blk << 22);
-  L.cramb = s.cram + (size_t)blk * (size_t)s.cram_stride * kEnvBlock;
-  L.rm = make_rsrc(L.memb, 1u << 22);
+  L.rm = make_rsrc(s.mem + ((size_t)blk << 22), 1u << 22);
+  L.memb = in_vgpr(s.mem + ((size_t)blk << 22));
+  L.cramb = in_vgpr(s.cram + (size_t)blk * (size_t)s.cram_stride * kEnvBlock);
+  L.rom = in_vgpr(s.rom);
+  L.rom_len = in_vgpr((uint32_t)s.rom_len);
   L.rsc = make_rsrc(s.sc + (size_t)blk * (kNumFields * kEnvBlock), kNumFields * kEnvBlock * 4);
   L.rcs = make_rsrc(s.cs + (size_t)blk * (kCartStateStride * kEnvBlock),
                     kCartStateStride * kEnvBlock * 4);
   const rsrc_t rcnt = make_rsrc(s.cnt + (size_t)blk * (2 * kEnvBlock), 2 * kEnvBlock * 8);
-  const uint2* recs = reinterpret_cast<const uint2*>(s.recs);
+  const uint2* recs = in_vgpr(reinterpret_cast<const uint2*>(s.recs));
 
   // ---- load (cpu_step_builder.py:930-967) ---------------------------------
   L.pc = (uint32_t)L.SC(F_PC) & 0xFFFFu;
@@ -685,7 +717,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   L.map_changed = 0;
   L.refresh_cart();
   L.action = args.actions[e];
-  L.release = args.release;
+  L.release = (int)in_vgpr((uint32_t)args.release);
   L.frames_done = 0;
 
   auto ld64 = [&](uint32_t slot) {
@@ -706,14 +738,17 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   int cframe = L.SC(F_CYCLE_IN_FRAME);
   int trap = L.SC(F_TRAP_FLAG), trap_pc = L.SC(F_TRAP_PC);
   int trap_op = L.SC(F_TRAP_OPCODE), trap_kind = L.SC(F_TRAP_KIND);
-  const uint32_t dbg_watch = (uint32_t)args.dbg_watch;
+  const uint32_t dbg_watch = in_vgpr((uint32_t)args.dbg_watch);
+  const uint32_t dbg_trap_pc = in_vgpr((uint32_t)args.dbg_trap_pc);
+  const uint32_t dbg_rst38 = in_vgpr((uint32_t)args.dbg_rst38);
+  const int dbg_max_instr = (int)in_vgpr((uint32_t)args.dbg_max_instr);
   auto watch_read = [&]() -> uint32_t {
     const uint32_t v = L.M(dbg_watch);
-    return dbg_watch >= 0xFF00u ? L.io_hot(dbg_watch, v) : v;
+    return Lane::io_derived(dbg_watch) ? L.io_fix(dbg_watch, v) : v;
   };
   const uint32_t watch_val = dbg_watch ? watch_read() : 0u;
-  const int frames = args.frames;
-  const bool dbg = args.dbg_rst38 || args.dbg_trap_pc || args.dbg_max_instr > 0 || dbg_watch;
+  const int frames = (int)in_vgpr((uint32_t)args.frames);
+  const bool dbg = args.dbg_rst38 || args.dbg_trap_pc || args.dbg_max_instr > 0 || args.dbg_watch;
 
   // record of the instruction at pc (valid when rv)
   uint32_t rlo = 0, rhi = 0;
@@ -745,11 +780,11 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       op = rlo & 0xFFu;
       const uint32_t b1 = (rlo >> 8) & 0xFFu, b2 = (rlo >> 16) & 0xFFu;
       if (dbg) {
-        if (args.dbg_trap_pc && pc == (uint32_t)args.dbg_trap_pc) {
+        if (dbg_trap_pc && pc == dbg_trap_pc) {
           if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5; }
           break;
         }
-        if (args.dbg_rst38 && op == 0xFFu && pc != 0x0038u) {
+        if (dbg_rst38 && op == 0xFFu && pc != 0x0038u) {
           if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 3; }
           break;
         }
@@ -772,15 +807,22 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       ra = sel(am == AM_C, 0xFF00u | (bc & 0xFFu), ra);
       uint32_t rd0 = 0, rd1 = 0;
       if (nr) {
-        // both loads issue before either is used; a lane with one read
-        // repeats its first address
-        const uint32_t x0 = Lane::fold(ra), x1 = Lane::fold(nr > 1u ? ra + 1u : ra);
-        bool o0, o1;
-        const uint8_t* p0 = L.bus_ptr(x0, &o0);
-        const uint8_t* p1 = L.bus_ptr(x1, &o1);
+        // Both loads issue before either is used.  The second byte (POP,
+        // RET) sits one address row (64 bytes) after the first when both
+        // are in the env's memory; a lane with one read repeats its first.
+        const uint32_t x0 = Lane::fold(ra);
+        const uint8_t* p0 = L.bus_ptr(x0);
+        uint32_t x1 = x0;
+        const uint8_t* p1 = p0;
+        if (nr > 1u) {
+          x1 = Lane::fold(ra + 1u);
+          p1 = p0 + kEnvBlock;
+          if (x1 != x0 + 1u || x0 < 0x8000u || x0 - 0xA000u < 0x2000u || x1 - 0xA000u < 0x2000u)
+            p1 = L.bus_ptr(x1);
+        }
         const uint32_t v0 = *p0, v1 = *p1;
-        rd0 = L.bus_fix(x0, v0, o0);
-        rd1 = L.bus_fix(x1, v1, o1);
+        rd0 = L.bus_fix(x0, v0);
+        rd1 = L.bus_fix(x1, v1);
       }
 
       // ---- execute: 8-bit datapath (alu.py, loads.py, bitops.py) -----------------
@@ -949,7 +991,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       int tcyc = 20;
       if (pass == 0) {
         if (!hiter) {
-          if (dbg && args.dbg_rst38 && L.pc >= 0xFE00u) {
+          if (dbg && dbg_rst38 && L.pc >= 0xFE00u) {
             if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4; }
             stop = true;
             break;
@@ -960,7 +1002,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
           }
           ninstr += 1;
           if (dbg) {
-            if (args.dbg_max_instr > 0 && instr + ninstr - instr_start >= args.dbg_max_instr) {
+            if (dbg_max_instr > 0 && instr + ninstr - instr_start >= dbg_max_instr) {
               if (!trap) { trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6; }
               stop = true;
               break;
@@ -995,7 +1037,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       L.ime = 0;
       const uint32_t bit = pending & (0u - pending);
       const uint32_t vec = 0x40u + 8u * (uint32_t)__builtin_ctz(bit);
-      L.ifr &= ~bit & 0xFFu;
+      L.set_if(L.ifr & ~bit & 0xFFu);
       wn = 2;
       wa0 = (L.sp - 1u) & 0xFFFFu;
       wv0 = L.pc >> 8;
