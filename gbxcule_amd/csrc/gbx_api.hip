@@ -69,19 +69,18 @@ hipError_t dalloc(T** p, size_t count) {
 // 0xFF that an unmapped ROM bank reads (open bus).
 constexpr int64_t kOpenBusBytes = 0x4000;
 
-// Pre-decoded instruction records for the step kernel's fetch: one 64-bit
-// word per ROM byte and per boot-image byte (after the ROM), holding the
-// opcode and the next two bytes of the same image in bits 0-23 and the
-// 40-bit micro-op decode (gbx_decode.h) in bits 24-63.  Bytes past the end
-// of an image read as 0; the kernel only uses a record when all three bytes
-// lie inside one 16 KiB ROM window or inside the boot image.
-std::vector<uint64_t> build_records(const uint8_t* rom, int64_t rom_bytes, const uint8_t* boot) {
-  std::vector<uint64_t> r((size_t)rom_bytes + 0x100 + kOpenBusBytes);
+// Pre-decoded instruction records for the step kernel's fetch: one 128-bit
+// record (gbx_decode.h) per byte of the ROM buffer, built from that byte and
+// the next two bytes of the same image.  Bytes past the end of an image read
+// as 0; the kernel only uses a record when all three instruction bytes lie
+// inside one 16 KiB ROM window or inside the boot image.
+std::vector<Rec> build_records(const uint8_t* rom, int64_t rom_bytes, const uint8_t* boot) {
+  std::vector<Rec> r((size_t)(rom_bytes + 0x100 + kOpenBusBytes));
   auto fill = [&](const uint8_t* img, int64_t len, size_t base) {
     for (int64_t i = 0; i < len; ++i) {
       const uint32_t op = img[i], b1 = i + 1 < len ? img[i + 1] : 0u,
                      b2 = i + 2 < len ? img[i + 2] : 0u;
-      r[base + (size_t)i] = (uint64_t)(op | (b1 << 8) | (b2 << 16)) | (decode_insn(op, b1) << 24);
+      r[base + (size_t)i] = decode_insn(op, b1, b2);
     }
   };
   fill(rom, rom_bytes, 0);
@@ -182,13 +181,13 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   A(dalloc(&s.pix_packed, (size_t)num_envs * kDsWB * kDsH));
   A(dalloc(&s.latches, (size_t)9 * kScreenH));
   uint8_t *drom = nullptr, *dboot = nullptr;
-  uint64_t* drecs = nullptr;
+  Rec* drecs = nullptr;
   A(dalloc(&drom, (size_t)(rom_bytes + 0x100 + kOpenBusBytes)));
   A(dalloc(&dboot, (size_t)0x100));
   A(dalloc(&drecs, (size_t)(rom_bytes + 0x100 + kOpenBusBytes)));
   s.rom = drom;
   s.boot = dboot;
-  s.recs = drecs;
+  s.recs = reinterpret_cast<const uint4*>(drecs);
   A(dalloc(&c->snap.mem, (size_t)kMemSize));
   A(dalloc(&c->snap.cram, (size_t)s.cram_stride));
   A(dalloc(&c->snap.serial, (size_t)kSerialMax));
@@ -203,12 +202,12 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   }
   std::vector<uint64_t> k(kHashLen);
   for (int i = 0; i < kHashLen; ++i) k[i] = splitmix((uint64_t)i);
-  const std::vector<uint64_t> recs = build_records(rom, rom_bytes, boot);
+  const std::vector<Rec> recs = build_records(rom, rom_bytes, boot);
   A(hipMemcpy(drom, rom, (size_t)rom_bytes, hipMemcpyHostToDevice));
   A(hipMemcpy(drom + rom_bytes, boot, 0x100, hipMemcpyHostToDevice));
   A(hipMemset(drom + rom_bytes + 0x100, 0xFF, (size_t)kOpenBusBytes));
   A(hipMemcpy(dboot, boot, 0x100, hipMemcpyHostToDevice));
-  A(hipMemcpy(drecs, recs.data(), recs.size() * sizeof(uint64_t), hipMemcpyHostToDevice));
+  A(hipMemcpy(drecs, recs.data(), recs.size() * sizeof(Rec), hipMemcpyHostToDevice));
   A(hipMemcpy(c->hash_k, k.data(), k.size() * 8, hipMemcpyHostToDevice));
   if (e != hipSuccess) {
     free_ctx(c);

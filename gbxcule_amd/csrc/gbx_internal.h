@@ -82,7 +82,7 @@ struct DevState {
   uint8_t* latches;     // [9][144] env-0 scanline latches
   const uint8_t* rom;       // ROM image, the 256-byte boot image, 16 KiB of 0xFF (open bus)
   const uint8_t* boot;
-  const uint64_t* recs;     // pre-decoded instruction per byte of the ROM buffer
+  const uint4* recs;        // pre-decoded instruction record per byte of the ROM buffer
   int n, npad, obs_dim;
   int rom_banks, rom_mask, ram_banks, ram_bytes, cram_stride, mbc_kind;
   int step_lanes;       // envs per step-kernel wavefront: 64, 32, 16 or 8

@@ -26,8 +26,9 @@
 //  * a halted CPU advances in one step to the next cycle at which anything it
 //    can observe changes (a PPU mode boundary, a timer reload, the frame end),
 //    which is exactly equivalent to the reference's 4-cycle halted loop.
-#include "gbx_decode.h"
 #include "gbx_internal.h"
+// after gbx_internal.h, which brings in the HIP runtime
+#include "gbx_exec.h"
 
 namespace gbx {
 namespace {
@@ -40,7 +41,7 @@ constexpr int kRtcCyclesPerSecond = 4194304;
 // Decode of instructions fetched outside the pre-decoded images (code in
 // RAM, the last two bytes of a ROM window): [op] or [256 + CB byte].
 struct DecTable {
-  uint64_t e[512];
+  Rec e[512];
 };
 constexpr DecTable make_dec_table() {
   DecTable t{};
@@ -159,15 +160,8 @@ struct Lane {
     return Ref8{rm, (addr << kEnvBlockShift) | lane, 0};
   }
 
-  // -- register file ---------------------------------------------------------
+  // -- register file (w0 = B C D E, w1 = H L - A) -------------------------------
   __device__ uint32_t a() const { return w1 & 0xFFu; }
-  __device__ uint32_t hl() const { return w1 >> 16; }
-  __device__ uint32_t bc() const { return w0 >> 16; }
-  __device__ uint32_t de() const { return w0 & 0xFFFFu; }
-  // 8-bit register idx in B C D E H L - A order (6 is never a register)
-  __device__ uint32_t r8(uint32_t idx) const {
-    return ((idx & 4u ? w1 : w0) >> (((idx & 3u) ^ 3u) << 3)) & 0xFFu;
-  }
 
   // -- cartridge windows (reference read8 ROM/RAM branches, :565-656) ----------
   __device__ static int clamp_bank(int bank, int count, int mask) {
@@ -646,18 +640,18 @@ struct Lane {
                                    : (p < 0x4000u ? rom_lo : rom_hi) + (p & 0x3FFFu);
   }
   // Fetch + decode through the bus (code in RAM, window edges, open bus).
-  __device__ void fetch_slow(uint32_t& rlo, uint32_t& rhi) const {
+  __device__ Rec fetch_slow() const {
     const uint32_t b0 = read8(pc), b1 = read8(pc + 1u), b2 = read8(pc + 2u);
-    const uint64_t d = kDec.e[b0 == 0xCBu ? 256u + b1 : b0];
-    rlo = b0 | (b1 << 8) | (b2 << 16) | ((uint32_t)d << 24);
-    rhi = (uint32_t)(d >> 8);
+    Rec r = kDec.e[b0 == 0xCBu ? 256u + b1 : b0];
+    r.w0 |= b0 | (b1 << 8) | (b2 << 16);
+    return r;
   }
 };
 
 // ---------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void step_kernel(DevState s, StepArgs args) {
   const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (uint32_t)s.n) return;
   Lane L{s};
@@ -673,7 +667,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   L.rcs = make_rsrc(s.cs + (size_t)blk * (kCartStateStride * kEnvBlock),
                     kCartStateStride * kEnvBlock * 4);
   const rsrc_t rcnt = make_rsrc(s.cnt + (size_t)blk * (2 * kEnvBlock), 2 * kEnvBlock * 8);
-  const uint2* recs = in_vgpr(reinterpret_cast<const uint2*>(s.recs));
+  const uint4* recs = in_vgpr(reinterpret_cast<const uint4*>(s.recs));
 
   // ---- load (cpu_step_builder.py:930-967) ---------------------------------
   L.pc = (uint32_t)L.SC(F_PC) & 0xFFFFu;
@@ -751,7 +745,7 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
   const bool dbg = args.dbg_rst38 || args.dbg_trap_pc || args.dbg_max_instr > 0 || args.dbg_watch;
 
   // record of the instruction at pc (valid when rv)
-  uint32_t rlo = 0, rhi = 0;
+  uint4 rec = uint4{0u, 0u, 0u, 0u};
   bool rv = false;
 
   while (L.frames_done < frames) {
@@ -769,16 +763,13 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
       // ---- fetch + decode ------------------------------------------------------
       const uint32_t pc = L.pc;
       if (!rv) {
-        if (L.rec_ok(pc)) {
-          const uint2 r = recs[L.rec_index(pc)];
-          rlo = r.x;
-          rhi = r.y;
-        } else {
-          L.fetch_slow(rlo, rhi);
+        if (L.rec_ok(pc)) rec = recs[L.rec_index(pc)];
+        else {
+          const Rec r = L.fetch_slow();
+          rec = uint4{r.w0, r.w1, r.w2, r.w3};
         }
       }
-      op = rlo & 0xFFu;
-      const uint32_t b1 = (rlo >> 8) & 0xFFu, b2 = (rlo >> 16) & 0xFFu;
+      op = rec.x & 0xFFu;
       if (dbg) {
         if (dbg_trap_pc && pc == dbg_trap_pc) {
           if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5; }
@@ -789,193 +780,63 @@ __global__ __launch_bounds__(64) void step_kernel(DevState s, StepArgs args) {
           break;
         }
       }
-      const uint32_t len = (rlo >> 24) & 3u, cyc4 = (rlo >> 26) & 7u, cycnt4 = rlo >> 29;
-      const uint32_t am = rhi & 7u, nr = (rhi >> 3) & 3u, hlinc = (rhi >> 5) & 3u;
-      const uint32_t src = (rhi >> 7) & 15u, dst = (rhi >> 11) & 7u, xa = (rhi >> 14) & 1u;
-      const uint32_t alu = (rhi >> 15) & 31u, aux = (rhi >> 20) & 7u, op16 = (rhi >> 23) & 31u;
-      const uint32_t rr = (rhi >> 28) & 3u, tp = rhi >> 30;
-      const uint32_t imm16 = b1 | (b2 << 8);
-      const uint32_t sp = L.sp, hl = L.hl(), bc = L.bc(), de = L.de();
+      ExecIn in;
+      in.rec = Rec{rec.x, rec.y, rec.z, rec.w};
+      in.w0 = L.w0;
+      in.w1 = L.w1;
+      in.f = L.f;
+      in.sp = L.sp;
+      in.pc = pc;
+      in.ra = operand_address(in.rec, L.w0, L.w1, L.sp);
 
-      // ---- operand address + bus reads ----------------------------------------
-      uint32_t ra = sp;
-      ra = sel(am == AM_HL, hl, ra);
-      ra = sel(am == AM_BC, bc, ra);
-      ra = sel(am == AM_DE, de, ra);
-      ra = sel(am == AM_A16, imm16, ra);
-      ra = sel(am == AM_A8, 0xFF00u | b1, ra);
-      ra = sel(am == AM_C, 0xFF00u | (bc & 0xFFu), ra);
-      uint32_t rd0 = 0, rd1 = 0;
+      // ---- bus reads ------------------------------------------------------------
+      const uint32_t nr = (rec.z >> 16) & 3u;
+      in.rd0 = 0;
+      in.rd1 = 0;
       if (nr) {
         // Both loads issue before either is used.  The second byte (POP,
         // RET) sits one address row (64 bytes) after the first when both
         // are in the env's memory; a lane with one read repeats its first.
-        const uint32_t x0 = Lane::fold(ra);
+        const uint32_t x0 = Lane::fold(in.ra);
         const uint8_t* p0 = L.bus_ptr(x0);
         uint32_t x1 = x0;
         const uint8_t* p1 = p0;
         if (nr > 1u) {
-          x1 = Lane::fold(ra + 1u);
+          x1 = Lane::fold(in.ra + 1u);
           p1 = p0 + kEnvBlock;
           if (x1 != x0 + 1u || x0 < 0x8000u || x0 - 0xA000u < 0x2000u || x1 - 0xA000u < 0x2000u)
             p1 = L.bus_ptr(x1);
         }
         const uint32_t v0 = *p0, v1 = *p1;
-        rd0 = L.bus_fix(x0, v0);
-        rd1 = L.bus_fix(x1, v1);
+        in.rd0 = L.bus_fix(x0, v0);
+        in.rd1 = L.bus_fix(x1, v1);
       }
 
-      // ---- execute: 8-bit datapath (alu.py, loads.py, bitops.py) -----------------
-      const uint32_t av = L.a(), fl = L.f, cin = (fl >> 4) & 1u;
-      const uint32_t yv = src == R_MEM ? rd0 : src == S_IMM ? b1 : L.r8(src);
-      const uint32_t xv = xa ? av : (dst == R_MEM ? rd0 : L.r8(dst));
-      // add/subtract unit: ADD ADC SUB SBC CP INC DEC
-      const bool is_sub = alu == A_SUB || alu == A_SBC || alu == A_CP || alu == A_DEC;
-      const bool incdec = alu == A_INC || alu == A_DEC;
-      const uint32_t yy = incdec ? 1u : yv;
-      const uint32_t ci = (alu == A_ADC || alu == A_SBC) ? cin : 0u;
-      const uint32_t sum = is_sub ? xv - (yy + ci) : xv + (yy + ci);
-      const uint32_t hsum = is_sub ? (xv & 15u) - ((yy & 15u) + ci) : (xv & 15u) + ((yy & 15u) + ci);
-      const uint32_t r_as = sum & 0xFFu;
-      const uint32_t f_as = ((uint32_t)(r_as == 0u) << 7) | ((uint32_t)is_sub << 6) |
-                            (((hsum >> 4) & 1u) << 5) | ((incdec ? cin : (sum >> 8) & 1u) << 4);
-      // shifter: RLC RRC RL RR SLA SRA SWAP SRL (CB) and RLCA RRCA RLA RRA
-      const uint32_t rk = (alu - A_RLC) & 7u;
-      const bool left = rk == 0u || rk == 2u || rk == 4u;
-      const uint32_t inl = rk == 0u ? xv >> 7 : rk == 2u ? cin : 0u;
-      const uint32_t inr = rk == 1u ? xv & 1u : rk == 3u ? cin : rk == 5u ? xv >> 7 : 0u;
-      uint32_t r_rot = left ? ((xv << 1) | inl) & 0xFFu : (xv >> 1) | (inr << 7);
-      r_rot = rk == 6u ? ((xv & 15u) << 4) | (xv >> 4) : r_rot;
-      const uint32_t c_rot = left ? xv >> 7 : rk == 6u ? 0u : xv & 1u;
-      const uint32_t f_rot = ((uint32_t)(alu < A_RLCA && r_rot == 0u) << 7) | (c_rot << 4);
-      // BIT / RES / SET
-      const uint32_t bm = 1u << aux;
-      // DAA (alu.py:897-950)
-      const uint32_t nf = (fl >> 6) & 1u, hf = (fl >> 5) & 1u;
-      const bool dlo = nf ? hf != 0u : (hf != 0u || (xv & 15u) > 9u);
-      const bool dhi = nf ? cin != 0u : (cin != 0u || xv > 0x99u);
-      const uint32_t adj = (dlo ? 0x06u : 0u) | (dhi ? 0x60u : 0u);
-      const uint32_t r_daa = (nf ? xv - adj : xv + adj) & 0xFFu;
-      // result + flags
-      uint32_t res = yv, f8 = fl;
-      res = alu - A_ADD < 7u ? r_as : res;
-      f8 = alu - A_ADD < 7u ? f_as : f8;
-      res = alu == A_AND ? (xv & yv) : res;
-      res = alu == A_XOR ? (xv ^ yv) : res;
-      res = alu == A_OR ? (xv | yv) : res;
-      f8 = alu - A_AND < 3u ? ((uint32_t)(res == 0u) << 7) | (alu == A_AND ? 0x20u : 0u) : f8;
-      res = alu - A_RLC < 12u ? r_rot : res;
-      f8 = alu - A_RLC < 12u ? f_rot : f8;
-      f8 = alu == A_BIT ? ((uint32_t)((xv & bm) == 0u) << 7) | 0x20u | (fl & 0x10u) : f8;
-      res = alu == A_RES ? xv & ~bm : res;
-      res = alu == A_SET ? xv | bm : res;
-      res = alu == A_DAA ? r_daa : res;
-      f8 = alu == A_DAA ? ((uint32_t)(r_daa == 0u) << 7) | (nf << 6) | ((dhi ? 1u : 0u) << 4) : f8;
-      res = alu == A_CPL ? xv ^ 0xFFu : res;
-      f8 = alu == A_CPL ? (fl & 0x90u) | 0x60u : f8;
-      res = alu >= A_SCF ? xv : res;
-      f8 = alu == A_SCF ? (fl & 0x80u) | 0x10u : f8;
-      f8 = alu == A_CCF ? (fl & 0x80u) | ((cin ^ 1u) << 4) : f8;
-      res &= 0xFFu;
-      const bool wb8 = alu != A_NONE && alu != A_CP && alu != A_BIT;
-      // register writeback (dst 6 is the bus operand: written below)
-      {
-        const uint32_t sh = ((dst & 3u) ^ 3u) << 3;
-        const uint32_t m = 0xFFu << sh;
-        const uint32_t nw = ((dst & 4u ? L.w1 : L.w0) & ~m) | (res << sh);
-        const bool reg = wb8 && dst != R_MEM;
-        L.w1 = (reg && (dst & 4u)) ? nw : L.w1;
-        L.w0 = (reg && !(dst & 4u)) ? nw : L.w0;
-      }
-      if (wb8 && dst == R_MEM) {
-        wn = 1;
-        wa0 = ra;
-        wv0 = res;
-      }
-      if (hlinc) L.w1 = (L.w1 & 0xFFFFu) | (((hlinc == 1u ? ra + 1u : ra - 1u) & 0xFFFFu) << 16);
-
-      // ---- execute: 16-bit, stack and control flow (alu.py, stack.py, jumps.py) --
-      const uint32_t rrv = rr == 0u ? bc : rr == 1u ? de : rr == 2u ? hl
-                           : op16 == O_PUSH ? ((av << 8) | fl) : sp;
-      const uint32_t e8 = (uint32_t)(int32_t)(int8_t)b1;
-      const uint32_t spe = (sp + e8) & 0xFFFFu;
-      const uint32_t rd16 = rd0 | (rd1 << 8);
-      uint32_t v16 = rd16;  // O_POP
-      v16 = op16 == O_LDRR ? imm16 : v16;
-      v16 = op16 == O_INCRR ? rrv + 1u : v16;
-      v16 = op16 == O_DECRR ? rrv - 1u : v16;
-      v16 = op16 == O_ADDHL ? hl + rrv : v16;
-      v16 = op16 == O_MOV16 ? rrv : v16;
-      v16 = (op16 == O_ADDSP || op16 == O_LDHLSP) ? spe : v16;
-      v16 &= 0xFFFFu;
-      const bool pop_af = op16 == O_POP && tp == 3u;
-      const bool wr16 = (op16 >= O_LDRR && op16 <= O_LDHLSP) || (op16 == O_POP && !pop_af);
-      {
-        const bool t0 = wr16 && tp == 0u, t1 = wr16 && tp == 1u, t2 = wr16 && tp == 2u;
-        L.w0 = t0 ? (L.w0 & 0xFFFFu) | (v16 << 16) : L.w0;
-        L.w0 = t1 ? (L.w0 & 0xFFFF0000u) | v16 : L.w0;
-        L.w1 = t2 ? (L.w1 & 0xFFFFu) | (v16 << 16) : L.w1;
-        L.w1 = pop_af ? (L.w1 & 0xFFFFFF00u) | rd1 : L.w1;
-      }
-      uint32_t fn = alu != A_NONE ? f8 : fl;
-      fn = op16 == O_ADDHL ? (fl & 0x80u) | ((uint32_t)(((hl & 0xFFFu) + (rrv & 0xFFFu)) > 0xFFFu) << 5) |
-                                 ((uint32_t)(hl + rrv > 0xFFFFu) << 4)
-                           : fn;
-      fn = (op16 == O_ADDSP || op16 == O_LDHLSP)
-               ? ((uint32_t)(((sp & 15u) + (b1 & 15u)) > 15u) << 5) |
-                     ((uint32_t)(((sp & 0xFFu) + b1) > 0xFFu) << 4)
-               : fn;
-      fn = pop_af ? rd0 & 0xF0u : fn;
-      L.f = fn & 0xF0u;
-      // branch condition: 0 always, 1 NZ, 2 Z, 3 NC, 4 C (tested on the flags
-      // the instruction started with)
-      const uint32_t cbit = aux <= 2u ? (fl >> 7) & 1u : (fl >> 4) & 1u;
-      const bool is_jump = op16 - O_JR <= (uint32_t)(O_RST - O_JR);
-      const bool taken = !is_jump || aux == 0u || cbit == (uint32_t)((aux & 1u) == 0u);
-      const uint32_t seq = (pc + len) & 0xFFFFu;
-      uint32_t target = imm16;  // JP, CALL
-      target = op16 == O_JR ? (pc + 2u + e8) & 0xFFFFu : target;
-      target = op16 == O_JPHL ? hl : target;
-      target = (op16 == O_RET || op16 == O_RETI) ? rd16 : target;
-      target = op16 == O_RST ? op & 0x38u : target;
-      const bool trapop = op16 == O_TRAP;
-      uint32_t npc = (is_jump && taken) ? target : seq;
-      npc = trapop ? pc : npc;
-      cycles = (int)((taken ? cyc4 : cycnt4) << 2);
-      // stack traffic
-      const bool push = op16 == O_PUSH || ((op16 == O_CALL || op16 == O_RST) && taken);
-      const uint32_t pushv = op16 == O_PUSH ? rrv : seq;
-      const bool stsp = op16 == O_STSP;
-      if (push || stsp) {
-        wn = 2;
-        wa0 = stsp ? imm16 : (sp - 1u) & 0xFFFFu;
-        wv0 = stsp ? sp & 0xFFu : pushv >> 8;
-        wa1 = stsp ? (imm16 + 1u) & 0xFFFFu : (sp - 2u) & 0xFFFFu;
-        wv1 = stsp ? (sp >> 8) & 0xFFu : pushv & 0xFFu;
-      }
-      uint32_t nsp = sp;
-      nsp = push ? (sp - 2u) & 0xFFFFu : nsp;
-      nsp = (op16 == O_POP || ((op16 == O_RET || op16 == O_RETI) && taken)) ? (sp + 2u) & 0xFFFFu : nsp;
-      nsp = (wr16 && tp == 3u) ? v16 : nsp;
-      L.sp = nsp;
-      // interrupt enable, HALT (misc.py)
-      const bool ime_on = op16 == O_EI || op16 == O_RETI;
-      const bool ime_set = ime_on || op16 == O_DI;
-      L.ime = ime_set ? (ime_on ? 1u : 0u) : L.ime;
-      L.ime_delay = ime_set ? 0u : L.ime_delay;
-      L.halted = op16 == O_HALT ? 1u : L.halted;
-      if (trapop && !trap) {  // misc.py:42-56: freeze the env, pc unchanged
+      // ---- execute (gbx_exec.h) -------------------------------------------------
+      const ExecOut o = exec_insn(in);
+      L.w0 = o.w0;
+      L.w1 = o.w1;
+      L.f = o.f;
+      L.sp = o.sp;
+      cycles = (int)o.cycles;
+      wn = o.wn;
+      wa0 = o.wa0;
+      wv0 = o.wv0;
+      wa1 = o.wa1;
+      wv1 = o.wv1;
+      L.ime = o.ime_set ? o.ime_on : L.ime;
+      L.ime_delay = o.ime_set ? 0u : L.ime_delay;
+      L.halted = o.halt ? 1u : L.halted;
+      if (o.trap && !trap) {  // misc.py:42-56: freeze the env, pc unchanged
         trap = 1;
         trap_pc = (int)pc;
         trap_op = (int)op;
         trap_kind = 1;
       }
-      L.pc = npc;
+      L.pc = o.npc;
       // fetch the next record while the writes, timer and PPU run
-      rv = L.rec_ok(npc);
-      const uint2 r = recs[rv ? L.rec_index(npc) : 0u];
-      rlo = r.x;
-      rhi = r.y;
+      rv = L.rec_ok(o.npc);
+      rec = recs[rv ? L.rec_index(o.npc) : 0u];
     } else {
       cycles = L.halt_cycles(cframe);
     }

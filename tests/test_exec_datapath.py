@@ -1,0 +1,175 @@
+"""The step kernel's instruction decode (gbx_decode.h) and straight-line
+datapath (gbx_exec.h), built for the host, against the oracle: every
+unprefixed and CB opcode from random register, flag and memory states.
+
+Bus operands are steered into WRAM/HRAM (address registers, SP, a8/a16
+immediates), so the bytes the datapath reads and writes are plain memory
+and the expected values come from the oracle's memory image.  The oracle
+runs exactly one instruction per env (debug max-instruction trap); the
+registers, F, SP, next pc, IME/HALT/trap and every byte of memory must then
+equal what the datapath produced.  Cycle counts are covered by the GPU
+parity tests, which compare cycle counters after whole frames.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import shutil
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from gbxcule_amd.carts.asm import ILLEGAL
+
+from ._isa import flat_rom, oracle, set_regs
+
+ROOT = Path(__file__).resolve().parent
+OPS = [op for op in range(256) if op != 0xCB] + [0x100 | cb for cb in range(256)]
+
+
+@pytest.fixture(scope="module")
+def harness(tmp_path_factory):
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    out = tmp_path_factory.mktemp("exec") / "exec_harness.so"
+    subprocess.run(
+        [gxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-o", str(out),
+         str(ROOT / "native" / "exec_harness.cpp")],
+        check=True,
+    )  # fmt: skip
+    lib = ctypes.CDLL(str(out))
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    lib.harness_decode.argtypes = [ctypes.c_uint32] * 3 + [u32p]
+    lib.harness_exec.argtypes = [u32p, u32p]
+    return lib
+
+
+def _arr(n):
+    return (ctypes.c_uint32 * n)()
+
+
+def _states(rng, n):
+    """Registers with every address register, SP and C pointing into RAM."""
+    r = {
+        "a": rng.integers(0, 256, n),
+        "b": rng.integers(0xC0, 0xE0, n),
+        "c": rng.integers(0x80, 0xFE, n),
+        "d": rng.integers(0xC0, 0xE0, n),
+        "e": rng.integers(0, 256, n),
+        "h": rng.integers(0xC0, 0xE0, n),
+        "l": rng.integers(0, 256, n),
+        "f": rng.integers(0, 16, n) << 4,
+        "sp": rng.integers(0xC004, 0xDFFC, n),
+        "ime": rng.integers(0, 2, n),
+    }
+    # HL, BC, DE + 1 must stay below E000 (echo RAM) for two-byte accesses
+    for hi, lo in (("h", "l"), ("b", "c"), ("d", "e")):
+        v = (r[hi] << 8) | r[lo]
+        r[lo] = np.where(v >= 0xDFFE, r[lo] & 0x7F, r[lo])
+    return r
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_datapath_matches_oracle(harness, seed):
+    rng = np.random.default_rng(seed)
+    ops = np.array(OPS * 3)
+    n = ops.size
+    pcs = 0x200 + 4 * np.arange(n)
+    b1 = rng.integers(0, 256, n)
+    b2 = rng.integers(0, 256, n)
+    for i, op in enumerate(ops):
+        if op in (0xEA, 0xFA, 0x08):  # a16 operand in WRAM
+            b2[i] = rng.integers(0xC0, 0xE0)
+            b1[i] = rng.integers(0, 0xFE)
+        elif op in (0xE0, 0xF0):  # a8 operand in HRAM
+            b1[i] = rng.integers(0x80, 0xFE)
+    blocks = {}
+    for i, op in enumerate(ops):
+        code = [0xCB, op & 0xFF, b2[i]] if op & 0x100 else [op, b1[i], b2[i]]
+        blocks[int(pcs[i])] = bytes(int(x) for x in code)
+    # CB opcodes: byte 1 is the CB sub-opcode, byte 2 the next byte
+    b1 = np.where(ops & 0x100, ops & 0xFF, b1)
+    rom = flat_rom(blocks)
+    m = oracle(rom, n, pcs)
+    regs = _states(rng, n)
+    set_regs(m, **regs)
+    m.mem[:, 0xC000:0xE000] = rng.integers(0, 256, (n, 0x2000), dtype=np.uint8)
+    m.mem[:, 0xFF80:0xFFFF] = rng.integers(0, 256, (n, 0x7F), dtype=np.uint8)
+    mem0 = m.mem.copy()
+    m.set_debug(max_instr=1)
+    m.step(None, frames=1, release=8)
+
+    rec, inp, out = _arr(4), _arr(11), _arr(16)
+    bad = []
+    for i, op in enumerate(ops):
+        opb = 0xCB if op & 0x100 else int(op)
+        harness.harness_decode(opb, int(b1[i]), int(b2[i]), rec)
+        w0 = (int(regs["b"][i]) << 24) | (int(regs["c"][i]) << 16) | (int(regs["d"][i]) << 8)
+        w0 |= int(regs["e"][i])
+        w1 = (int(regs["h"][i]) << 24) | (int(regs["l"][i]) << 16) | int(regs["a"][i])
+        sp = int(regs["sp"][i])
+        # operand address as the datapath computes it; the bytes there
+        for k in range(4):
+            inp[k] = rec[k]
+        inp[4], inp[5], inp[6], inp[7], inp[8] = w0, w1, int(regs["f"][i]), sp, int(pcs[i])
+        inp[9] = inp[10] = 0
+        harness.harness_exec(inp, out)
+        ra = out[0]
+        inp[9] = int(mem0[i, ra & 0xFFFF])
+        inp[10] = int(mem0[i, (ra + 1) & 0xFFFF])
+        harness.harness_exec(inp, out)
+        o = list(out)
+        want = {
+            "a": o[2] & 0xFF, "b": o[1] >> 24, "c": (o[1] >> 16) & 0xFF, "d": (o[1] >> 8) & 0xFF,
+            "e": o[1] & 0xFF, "h": o[2] >> 24, "l": (o[2] >> 16) & 0xFF, "f": o[3], "sp": o[4],
+            "pc": o[5],
+        }  # fmt: skip
+        ime = o[13] if o[12] else int(regs["ime"][i])
+        want["ime"] = ime
+        want["halted"] = o[14]
+        for name, v in want.items():
+            got = int(m.field(name)[i])
+            if got != v:
+                bad.append(f"op {op:#05x}: {name} datapath={v:#x} oracle={got:#x}")
+        exp = mem0[i].copy()
+        if o[7] > 2 or any(x > 0xFF for x in (o[9], o[11])):
+            bad.append(f"op {op:#05x}: bad write list {o[7:12]}")
+            continue
+        for k in range(o[7]):
+            a, v = (o[8], o[9]) if k == 0 else (o[10], o[11])
+            exp[a & 0xFFFF] = v
+        if not np.array_equal(exp, m.mem[i]):
+            d = np.nonzero(exp != m.mem[i])[0]
+            bad.append(f"op {op:#05x}: memory differs at {[hex(x) for x in d[:4]]}")
+        trapped = int(m.field("trap_kind")[i]) == 1
+        if bool(o[15]) != trapped or (trapped and op not in ILLEGAL | {0x10}):
+            bad.append(f"op {op:#05x}: trap datapath={o[15]} oracle kind={m.field('trap_kind')[i]}")
+    assert not bad, f"{len(bad)} mismatches:\n" + "\n".join(bad[:30])
+
+
+LEN3 = {0x01, 0x11, 0x21, 0x31, 0x08, 0xC2, 0xC3, 0xC4, 0xCA, 0xCC, 0xCD, 0xD2, 0xD4, 0xDA,
+        0xDC, 0xEA, 0xFA}  # fmt: skip
+LEN2 = {0x06, 0x0E, 0x16, 0x1E, 0x26, 0x2E, 0x36, 0x3E, 0x18, 0x20, 0x28, 0x30, 0x38, 0xC6,
+        0xCE, 0xD6, 0xDE, 0xE6, 0xEE, 0xF6, 0xFE, 0xE0, 0xF0, 0xE8, 0xF8}  # fmt: skip
+
+
+def test_record_cycles_and_lengths_match_opcode_table(harness):
+    """Length and both cycle counts of every record against the public SM83
+    opcode table (the same table the oracle's cycle-count test uses)."""
+    from .test_oracle_programs import LEGAL, table_cycles
+
+    rec = _arr(4)
+    for op in LEGAL:
+        harness.harness_decode(op, 0, 0, rec)
+        taken, not_taken = ((rec[0] >> 26) & 7) * 4, (rec[0] >> 29) * 4
+        assert (taken, not_taken) == table_cycles(op), f"op {op:#04x}"
+        exp_len = 3 if op in LEN3 else 2 if op in LEN2 else 1
+        assert (rec[0] >> 24) & 3 == exp_len, f"op {op:#04x} length"
+    for cb in range(256):
+        harness.harness_decode(0xCB, cb, 0, rec)
+        exp = 8 if cb & 7 != 6 else 12 if cb >> 6 == 1 else 16
+        assert ((rec[0] >> 26) & 7) * 4 == exp, f"cb {cb:#04x}"
+        assert (rec[0] >> 24) & 3 == 2
