@@ -757,7 +757,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     const uint32_t pc_before = L.pc;
     // pending bus writes: the instruction's, then the interrupt push
     uint32_t wn = 0, wa0 = 0, wv0 = 0, wa1 = 0, wv1 = 0;
-    bool stop = false;
 
     if (!hiter) {
       // ---- fetch + decode ------------------------------------------------------
@@ -841,75 +840,58 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       cycles = L.halt_cycles(cframe);
     }
 
-    // ---- write phase (instruction writes), then timer/PPU/IRQ; a serviced
-    // interrupt queues its two push writes and runs this block once more ----
+    // ---- write phase, debug checks, timer, PPU, interrupt check --------------
     int svc = 0;
-    uint32_t lcdc_now = L.lcdc;
-#pragma unroll 1
-    for (int pass = 0; pass < 2; ++pass) {
-      if (wn >= 1u) L.write8(wa0, wv0);
-      if (wn >= 2u) L.write8(wa1, wv1);
-      int tcyc = 20;
-      if (pass == 0) {
-        if (!hiter) {
-          if (dbg && dbg_rst38 && L.pc >= 0xFE00u) {
-            if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4; }
-            stop = true;
-            break;
-          }
-          if (trap) {
-            stop = true;
-            break;
-          }
-          ninstr += 1;
-          if (dbg) {
-            if (dbg_max_instr > 0 && instr + ninstr - instr_start >= dbg_max_instr) {
-              if (!trap) { trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6; }
-              stop = true;
-              break;
-            }
-            if (dbg_watch && watch_read() != watch_val) {
-              if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 7; }
-              stop = true;
-              break;
-            }
-          }
-        }
-        tcyc = cycles;
-      }
-      L.timer_tick(tcyc);
-      if (pass == 0 && !hiter && L.ime_delay) {
-        L.ime = 1;
-        L.ime_delay = 0;
-      }
-      lcdc_now = L.ppu_advance(tcyc);
-      if (pass == 1) break;
-      const uint32_t pending = L.ie & L.ifr & 0x1Fu;
-      if (!pending) break;
-      L.halted = 0;
-      if (!L.ime) {
-        if (hiter) {
-          L.pc = (L.pc + 1u) & 0xFFFFu;  // IME=0 wake skips a byte
-          rv = false;
-        }
+    if (wn >= 1u) L.write8(wa0, wv0);
+    if (wn >= 2u) L.write8(wa1, wv1);
+    if (!hiter) {
+      if (dbg && dbg_rst38 && L.pc >= 0xFE00u) {
+        if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4; }
         break;
       }
-      // service (cpu_step_builder.py:1502-1600)
-      L.ime = 0;
-      const uint32_t bit = pending & (0u - pending);
-      const uint32_t vec = 0x40u + 8u * (uint32_t)__builtin_ctz(bit);
-      L.set_if(L.ifr & ~bit & 0xFFu);
-      wn = 2;
-      wa0 = (L.sp - 1u) & 0xFFFFu;
-      wv0 = L.pc >> 8;
-      wa1 = (L.sp - 2u) & 0xFFFFu;
-      wv1 = L.pc & 0xFFu;
-      L.sp = wa1;
-      L.pc = vec;
-      rv = false;
-      svc = 20;
+      if (trap) break;
+      ninstr += 1;
+      if (dbg) {
+        if (dbg_max_instr > 0 && instr + ninstr - instr_start >= dbg_max_instr) {
+          if (!trap) { trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6; }
+          break;
+        }
+        if (dbg_watch && watch_read() != watch_val) {
+          if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 7; }
+          break;
+        }
+      }
     }
-    if (stop) break;
+    L.timer_tick(cycles);
+    if (!hiter && L.ime_delay) {
+      L.ime = 1;
+      L.ime_delay = 0;
+    }
+    uint32_t lcdc_now = L.ppu_advance(cycles);
+    const uint32_t pending = L.ie & L.ifr & 0x1Fu;
+    if (pending) {
+      L.halted = 0;
+      if (L.ime) {
+        // service (cpu_step_builder.py:1502-1600): push pc, jump to the
+        // vector, 20 cycles of timer and PPU
+        L.ime = 0;
+        const uint32_t bit = pending & (0u - pending);
+        L.set_if(L.ifr & ~bit & 0xFFu);
+        const uint32_t ret = L.pc;
+#pragma unroll 1
+        for (uint32_t k = 1; k <= 2; ++k)
+          L.write8((L.sp - k) & 0xFFFFu, k == 1 ? ret >> 8 : ret & 0xFFu);
+        L.sp = (L.sp - 2u) & 0xFFFFu;
+        L.pc = 0x40u + 8u * (uint32_t)__builtin_ctz(bit);
+        rv = false;
+        svc = 20;
+        L.timer_tick(20);
+        lcdc_now = L.ppu_advance(20);
+      } else if (hiter) {
+        L.pc = (L.pc + 1u) & 0xFFFFu;  // IME=0 wake skips a byte
+        rv = false;
+      }
+    }
     if (L.map_changed) {
       L.map_changed = 0;
       rv = false;
