@@ -748,8 +748,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   uint4 rec = uint4{0u, 0u, 0u, 0u};
   bool rv = false;
 
-  while (L.frames_done < frames) {
-    if (trap) break;
+  // One exit: the frame count reached or the env trapped (a trap freezes
+  // the env for the rest of the launch, misc.py:42-56).
+  while (L.frames_done < frames && !trap) {
     const uint32_t lcdc_prev = L.lcdc & 0x80u;
     const bool hiter = L.halted != 0;
     int cycles = 4;
@@ -769,16 +770,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
         }
       }
       op = rec.x & 0xFFu;
-      if (dbg) {
+      if (dbg) {  // debug traps before execution: the instruction does not run
         if (dbg_trap_pc && pc == dbg_trap_pc) {
-          if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5; }
-          break;
-        }
-        if (dbg_rst38 && op == 0xFFu && pc != 0x0038u) {
-          if (!trap) { trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 3; }
-          break;
+          trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5;
+        } else if (dbg_rst38 && op == 0xFFu && pc != 0x0038u) {
+          trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 3;
         }
       }
+      if (!trap) {
       ExecIn in;
       in.rec = Rec{rec.x, rec.y, rec.z, rec.w};
       in.w0 = L.w0;
@@ -836,6 +835,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       // fetch the next record while the writes, timer and PPU run
       rv = L.rec_ok(o.npc);
       rec = recs[rv ? L.rec_index(o.npc) : 0u];
+      }
     } else {
       cycles = L.halt_cycles(cframe);
     }
@@ -845,94 +845,92 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     if (wn >= 1u) L.write8(wa0, wv0);
     if (wn >= 2u) L.write8(wa1, wv1);
     if (!hiter) {
-      if (dbg && dbg_rst38 && L.pc >= 0xFE00u) {
-        if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4; }
-        break;
+      if (dbg && dbg_rst38 && L.pc >= 0xFE00u && !trap) {
+        trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4;
       }
-      if (trap) break;
-      ninstr += 1;
-      if (dbg) {
-        if (dbg_max_instr > 0 && instr + ninstr - instr_start >= dbg_max_instr) {
-          if (!trap) { trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6; }
-          break;
-        }
-        if (dbg_watch && watch_read() != watch_val) {
-          if (!trap) { trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 7; }
-          break;
+      if (!trap) {
+        ninstr += 1;
+        if (dbg) {
+          if (dbg_max_instr > 0 && instr + ninstr - instr_start >= dbg_max_instr) {
+            trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6;
+          } else if (dbg_watch && watch_read() != watch_val) {
+            trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 7;
+          }
         }
       }
     }
-    L.timer_tick(cycles);
-    if (!hiter && L.ime_delay) {
-      L.ime = 1;
-      L.ime_delay = 0;
-    }
-    uint32_t lcdc_now = L.ppu_advance(cycles);
-    const uint32_t pending = L.ie & L.ifr & 0x1Fu;
-    if (pending) {
-      L.halted = 0;
-      if (L.ime) {
-        // service (cpu_step_builder.py:1502-1600): push pc, jump to the
-        // vector, 20 cycles of timer and PPU
-        L.ime = 0;
-        const uint32_t bit = pending & (0u - pending);
-        L.set_if(L.ifr & ~bit & 0xFFu);
-        const uint32_t ret = L.pc;
+    if (!trap) {
+      L.timer_tick(cycles);
+      if (!hiter && L.ime_delay) {
+        L.ime = 1;
+        L.ime_delay = 0;
+      }
+      uint32_t lcdc_now = L.ppu_advance(cycles);
+      const uint32_t pending = L.ie & L.ifr & 0x1Fu;
+      if (pending) {
+        L.halted = 0;
+        if (L.ime) {
+          // service (cpu_step_builder.py:1502-1600): push pc, jump to the
+          // vector, 20 cycles of timer and PPU
+          L.ime = 0;
+          const uint32_t bit = pending & (0u - pending);
+          L.set_if(L.ifr & ~bit & 0xFFu);
+          const uint32_t ret = L.pc;
 #pragma unroll 1
-        for (uint32_t k = 1; k <= 2; ++k)
-          L.write8((L.sp - k) & 0xFFFFu, k == 1 ? ret >> 8 : ret & 0xFFu);
-        L.sp = (L.sp - 2u) & 0xFFFFu;
-        L.pc = 0x40u + 8u * (uint32_t)__builtin_ctz(bit);
-        rv = false;
-        svc = 20;
-        L.timer_tick(20);
-        lcdc_now = L.ppu_advance(20);
-      } else if (hiter) {
-        L.pc = (L.pc + 1u) & 0xFFFFu;  // IME=0 wake skips a byte
-        rv = false;
-      }
-    }
-    if (L.map_changed) {
-      L.map_changed = 0;
-      rv = false;
-    }
-
-    const int total = cycles + svc;
-    L.rtc_tick(total);
-    ncyc += (uint32_t)total;
-    cframe += total;
-    if (!(((lcdc_prev ^ lcdc_now) & 0x80u) || cframe >= kCyclesPerFrame)) continue;
-    // LCD toggles and frame ends (cpu_step_builder.py frame loop)
-    instr += ninstr;
-    cyc += ncyc;
-    ninstr = 0;
-    ncyc = 0;
-    if (lcdc_prev && !(lcdc_now & 0x80u)) {
-      int tail = 0;
-      if (!hiter) {
-        tail = total;
-        if (op == 0xE0u) {
-          const uint32_t imm = L.read8((pc_before + 1u) & 0xFFFFu);
-          if (imm == 0x40u && cycles >= 4) tail = total - 4;
+          for (uint32_t k = 1; k <= 2; ++k)
+            L.write8((L.sp - k) & 0xFFFFu, k == 1 ? ret >> 8 : ret & 0xFFu);
+          L.sp = (L.sp - 2u) & 0xFFFFu;
+          L.pc = 0x40u + 8u * (uint32_t)__builtin_ctz(bit);
+          rv = false;
+          svc = 20;
+          L.timer_tick(20);
+          lcdc_now = L.ppu_advance(20);
+        } else if (hiter) {
+          L.pc = (L.pc + 1u) & 0xFFFFu;  // IME=0 wake skips a byte
+          rv = false;
         }
       }
-      cframe = tail;
-      if (++L.frames_done >= frames) break;
-      continue;
-    }
-    if (!hiter && !lcdc_prev && (lcdc_now & 0x80u)) {
-      L.scan = 0;
-      L.ly = 0;
-      L.wl = 0;
-      L.lym = 0;
-      L.stat_fresh = 0;  // STAT and stat_prev follow from scan 0 of line 0
-      cframe = 0;
-      if (++L.frames_done >= frames) break;
-      continue;
-    }
-    while (cframe >= kCyclesPerFrame) {
-      cframe -= kCyclesPerFrame;
-      if (++L.frames_done >= frames) break;
+      if (L.map_changed) {
+        L.map_changed = 0;
+        rv = false;
+      }
+
+      const int total = cycles + svc;
+      L.rtc_tick(total);
+      ncyc += (uint32_t)total;
+      cframe += total;
+      if (((lcdc_prev ^ lcdc_now) & 0x80u) || cframe >= kCyclesPerFrame) {
+        // LCD toggles and frame ends (cpu_step_builder.py frame loop)
+        instr += ninstr;
+        cyc += ncyc;
+        ninstr = 0;
+        ncyc = 0;
+        if (lcdc_prev && !(lcdc_now & 0x80u)) {
+          int tail = 0;
+          if (!hiter) {
+            tail = total;
+            if (op == 0xE0u) {
+              const uint32_t imm = L.read8((pc_before + 1u) & 0xFFFFu);
+              if (imm == 0x40u && cycles >= 4) tail = total - 4;
+            }
+          }
+          cframe = tail;
+          ++L.frames_done;
+        } else if (!hiter && !lcdc_prev && (lcdc_now & 0x80u)) {
+          L.scan = 0;
+          L.ly = 0;
+          L.wl = 0;
+          L.lym = 0;
+          L.stat_fresh = 0;  // STAT and stat_prev follow from scan 0 of line 0
+          cframe = 0;
+          ++L.frames_done;
+        } else {
+          while (cframe >= kCyclesPerFrame && L.frames_done < frames) {
+            cframe -= kCyclesPerFrame;
+            ++L.frames_done;
+          }
+        }
+      }
     }
   }
   instr += ninstr;
