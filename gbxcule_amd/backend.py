@@ -589,11 +589,76 @@ class HipVecBackend:
         """Runtime form of the reference's GBXCULE_TRAP_* kernel switches."""
         self._call("gbx_set_debug", self.ctx, int(bool(rst38)), trap_pc, max_instr, watch_addr)
 
+    # -- savestates (reference warp_vec.py:1024-1074) ---------------------------
+    def _check_env(self, env_idx: int) -> None:
+        if not self._initialized:
+            raise RuntimeError("Backend not initialized. Call reset() first.")
+        if env_idx < 0 or env_idx >= self.num_envs:
+            raise ValueError(f"env_idx {env_idx} out of range [0, {self.num_envs})")
+
+    def export_env(self, env_idx: int):
+        """One env's scalars, cart state, memory and cart RAM (one device call)."""
+        from .state_io import EnvImage
+
+        self._check_env(env_idx)
+        img = EnvImage(
+            scalars=np.zeros(len(_lib.FIELDS), dtype=np.int64),
+            cart_state=np.zeros(CART_STATE_STRIDE, dtype=np.int32),
+            mem=np.zeros(MEM_SIZE, dtype=np.uint8),
+            cart_ram=np.zeros(self._info(_lib.INFO_RAM_BYTES), dtype=np.uint8),
+        )
+        p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+        self._call(
+            "gbx_export_env", self.ctx, env_idx, p(img.scalars), p(img.cart_state), p(img.mem),
+            p(img.cart_ram) if img.cart_ram.size else None,
+        )  # fmt: skip
+        return img
+
+    def import_env(self, env_idx: int, img) -> None:
+        """Write an ``EnvImage`` back into env ``env_idx`` (cart RAM and the
+        env-0 latches only when the image carries them)."""
+        self._check_env(env_idx)
+        sc = np.ascontiguousarray(img.scalars, dtype=np.int64)
+        cs = np.ascontiguousarray(img.cart_state, dtype=np.int32)
+        mem = np.ascontiguousarray(img.mem, dtype=np.uint8)
+        if sc.shape != (len(_lib.FIELDS),) or cs.shape != (CART_STATE_STRIDE,) or mem.shape != (MEM_SIZE,):
+            raise ValueError("env image has the wrong shape")
+        cram = np.ascontiguousarray(img.cart_ram, dtype=np.uint8)
+        if cram.size and cram.size != self._info(_lib.INFO_RAM_BYTES):
+            raise ValueError("cart RAM image has the wrong size")
+        lat = None if img.latches is None else np.ascontiguousarray(img.latches, dtype=np.uint8)
+        if lat is not None and lat.shape != (9, 144):
+            raise ValueError("latches must have shape (9, 144)")
+        p = lambda a: None if a is None or a.size == 0 else a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+        self._call("gbx_import_env", self.ctx, env_idx, p(sc), p(cs), p(mem), p(cram), p(lat))
+
+    def save_state(self, env_idx: int = 0):
+        """Env ``env_idx`` as a ``PyBoyState``."""
+        from .state_io import state_from_warp_backend
+
+        return state_from_warp_backend(self, env_idx)
+
     def save_state_file(self, path: str, env_idx: int = 0) -> None:
-        raise NotImplementedError("PyBoy savestate I/O is not part of this build")
+        """Write env ``env_idx`` to a PyBoy version-9 savestate file."""
+        from .state_io import save_pyboy_state, state_from_warp_backend
+
+        save_pyboy_state(state_from_warp_backend(self, env_idx), path)
+
+    def load_state(self, state, env_idx: int = 0) -> None:
+        """Load a ``PyBoyState`` into env ``env_idx``."""
+        from .state_io import apply_state_to_warp_backend
+
+        apply_state_to_warp_backend(state, self, env_idx)
 
     def load_state_file(self, path: str, env_idx: int = 0) -> None:
-        raise NotImplementedError("PyBoy savestate I/O is not part of this build")
+        """Load a PyBoy savestate file (versions 9-15) into env ``env_idx``."""
+        from .state_io import apply_state_to_warp_backend, load_pyboy_state
+
+        expected = 0
+        if self._rom_bytes is not None:
+            expected = int(parse_cartridge_header(self._rom_bytes).ram_byte_length)
+        state = load_pyboy_state(path, expected_cart_ram_size=expected)
+        apply_state_to_warp_backend(state, self, env_idx)
 
     def close(self) -> None:
         self._views.clear()

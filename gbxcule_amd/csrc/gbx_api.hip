@@ -469,6 +469,59 @@ int gbx_export_latches(gbx_ctx* ctx, uint8_t* host_out) {
   return GBX_OK;
 }
 
+int gbx_export_env(gbx_ctx* ctx, int32_t env, int64_t* scalars, int32_t* cart_state,
+                   uint8_t* mem, uint8_t* cart_ram) {
+  CHECK_CTX(ctx);
+  if (!scalars || !cart_state || !mem) return fail(GBX_E_INVALID, "out is NULL");
+  if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
+  const DevState& s = ctx->s;
+  const size_t nb = img_bytes(s.ram_bytes);
+  std::vector<uint8_t> h(nb);
+  uint8_t* img = nullptr;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMalloc(&img, nb));
+  hipError_t e = launch_env_image(s, env, img, 0, 0, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(h.data(), img, nb, hipMemcpyDeviceToHost);
+  (void)hipFree(img);
+  HIP_TRY(e);
+  memcpy(scalars, h.data(), sizeof(int64_t) * GBX_NUM_FIELDS);
+  memcpy(cart_state, h.data() + kImgCart, sizeof(int32_t) * kCartStateStride);
+  memcpy(mem, h.data() + kImgMem, kMemSize);
+  if (cart_ram && s.ram_bytes > 0) memcpy(cart_ram, h.data() + kImgCram, (size_t)s.ram_bytes);
+  return GBX_OK;
+}
+
+int gbx_import_env(gbx_ctx* ctx, int32_t env, const int64_t* scalars, const int32_t* cart_state,
+                   const uint8_t* mem, const uint8_t* cart_ram, const uint8_t* latches) {
+  CHECK_CTX(ctx);
+  if (!scalars || !cart_state || !mem) return fail(GBX_E_INVALID, "in is NULL");
+  if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
+  const DevState& s = ctx->s;
+  const size_t nb = img_bytes(s.ram_bytes);
+  std::vector<uint8_t> h(nb, 0);
+  memcpy(h.data(), scalars, sizeof(int64_t) * GBX_NUM_FIELDS);
+  memcpy(h.data() + kImgCart, cart_state, sizeof(int32_t) * kCartStateStride);
+  memcpy(h.data() + kImgMem, mem, kMemSize);
+  int parts = 0;
+  if (cart_ram && s.ram_bytes > 0) {
+    memcpy(h.data() + kImgCram, cart_ram, (size_t)s.ram_bytes);
+    parts |= IMG_CRAM;
+  }
+  if (latches) {
+    memcpy(h.data() + img_latches_off(s.ram_bytes), latches, kLatchBytes);
+    parts |= IMG_LATCHES;
+  }
+  uint8_t* img = nullptr;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMalloc(&img, nb));
+  hipError_t e = hipMemcpy(img, h.data(), nb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_env_image(s, env, img, 1, parts, nullptr);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  (void)hipFree(img);
+  HIP_TRY(e);
+  return GBX_OK;
+}
+
 int gbx_buffer(gbx_ctx* ctx, int32_t which, void** dev_ptr, int64_t* nbytes) {
   CHECK_CTX(ctx);
   if (!dev_ptr || !nbytes) return fail(GBX_E_INVALID, "out is NULL");

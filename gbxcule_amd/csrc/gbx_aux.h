@@ -16,6 +16,23 @@ struct SnapState {
   int has_pix;
 };
 
+// One env's whole state as one flat byte image (state save/load):
+//   [0, 256)           int64 per-env scalars in GBX_FIELD_* order
+//   [256, 336)         int32 cart state, 20 slots
+//   [512, 512 + 64K)   raw memory
+//   then ram_bytes of cart RAM, then the 9 x 144 env-0 scanline latches.
+constexpr size_t kImgCart = 256;
+constexpr size_t kImgMem = 512;
+constexpr size_t kImgCram = kImgMem + kMemSize;
+constexpr int kLatchBytes = 9 * kScreenH;
+__host__ __device__ inline size_t img_latches_off(int ram_bytes) { return kImgCram + (size_t)ram_bytes; }
+__host__ __device__ inline size_t img_bytes(int ram_bytes) { return img_latches_off(ram_bytes) + kLatchBytes; }
+enum { IMG_CRAM = 1, IMG_LATCHES = 2 };
+// to_device = 0: gather env into img (every part); 1: scatter img into env
+// (scalars, cart state and memory always; cart RAM / latches per `parts`).
+hipError_t launch_env_image(const DevState& s, int env, uint8_t* img, int to_device, int parts,
+                            hipStream_t st);
+
 hipError_t launch_snapshot(const DevState& s, const SnapState& snap, int env, int with_pix,
                            hipStream_t st);
 hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const uint8_t* mask,

@@ -271,7 +271,55 @@ __global__ void export_cram_kernel(DevState s, uint32_t env_lo, uint32_t count, 
   dst[i] = s.cram[cram_index(env_lo + ei, off, stride)];
 }
 
+// One thread per element of the image: 32 scalars, 20 cart slots, then the
+// bytes of memory, cart RAM and latches.
+__global__ void env_image_kernel(DevState s, uint32_t env, uint8_t* img, int to_device,
+                                 int parts) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t ram = (uint32_t)s.ram_bytes;
+  const uint32_t n_mem = 52u + (uint32_t)kMemSize;
+  int64_t* isc = reinterpret_cast<int64_t*>(img);
+  int32_t* ics = reinterpret_cast<int32_t*>(img + kImgCart);
+  if (i < 32u) {
+    const int f = (int)i;
+    if (f == F_INSTR || f == F_CYCLES) {
+      int64_t& d = s.cnt[cnt_index(env, f - F_INSTR)];
+      if (to_device) d = isc[f]; else isc[f] = d;
+    } else if (f == F_ACTIONS) {
+      if (to_device) s.actions[env] = (int32_t)isc[f]; else isc[f] = s.actions[env];
+    } else {
+      int32_t& d = s.sc[sc_index(env, f)];
+      if (to_device) d = (int32_t)isc[f]; else isc[f] = d;
+    }
+  } else if (i < 52u) {
+    int32_t& d = s.cs[cs_index(env, (int)(i - 32u))];
+    if (to_device) d = ics[i - 32u]; else ics[i - 32u] = d;
+  } else if (i < n_mem) {
+    const uint32_t a = i - 52u;
+    uint8_t& d = s.mem[mem_index(env, a)];
+    if (to_device) d = img[kImgMem + a]; else img[kImgMem + a] = d;
+  } else if (i < n_mem + ram) {
+    const uint32_t off = i - n_mem;
+    uint8_t& d = s.cram[cram_index(env, off, (uint32_t)s.cram_stride)];
+    if (!to_device) img[kImgCram + off] = d;
+    else if (parts & IMG_CRAM) d = img[kImgCram + off];
+  } else if (i < n_mem + ram + (uint32_t)kLatchBytes) {
+    const uint32_t k = i - n_mem - ram;
+    uint8_t* src = img + img_latches_off((int)ram);
+    if (!to_device) src[k] = s.latches[k];
+    else if (parts & IMG_LATCHES) s.latches[k] = src[k];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_env_image(const DevState& s, int env, uint8_t* img, int to_device, int parts,
+                            hipStream_t st) {
+  const uint32_t total = 52u + (uint32_t)kMemSize + (uint32_t)s.ram_bytes + (uint32_t)kLatchBytes;
+  hipLaunchKernelGGL(env_image_kernel, dim3((total + 255) / 256), dim3(256), 0, st, s,
+                     (uint32_t)env, img, to_device, parts);
+  return hipGetLastError();
+}
 
 hipError_t launch_reset(const DevState& s, hipStream_t st) {
   const size_t mem_bytes = (size_t)s.npad * kMemSize;

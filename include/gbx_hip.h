@@ -136,6 +136,22 @@ int gbx_export_cart_ram(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi,
 int gbx_export_serial(gbx_ctx* ctx, uint8_t* host_out);
 int gbx_export_latches(gbx_ctx* ctx, uint8_t* host_out);
 
+/* One env's whole state in one synchronous call: scalars[GBX_NUM_FIELDS]
+ * (GBX_FIELD_* order), cart_state[20], mem[65536] raw memory image and
+ * cart_ram[GBX_INFO_RAM_BYTES] (NULL: not copied).  This is the device side
+ * of state_from_warp_backend / apply_state_to_warp_backend
+ * (core/state_io.py:662-837, 839-1154), which the reference does with one
+ * Warp array copy per field; the savestate file format itself is host code
+ * (gbxcule_amd/state_io.py).  gbx_import_env writes every scalar, slot and
+ * memory byte given; cart_ram and the env-0 scanline latches (latches[9*144],
+ * order LCDC, SCX, SCY, BGP, WX, WY, window line, OBP0, OBP1) are written
+ * only when non-NULL. */
+int gbx_export_env(gbx_ctx* ctx, int32_t env, int64_t* scalars, int32_t* cart_state,
+                   uint8_t* mem, uint8_t* cart_ram);
+int gbx_import_env(gbx_ctx* ctx, int32_t env, const int64_t* scalars,
+                   const int32_t* cart_state, const uint8_t* mem,
+                   const uint8_t* cart_ram, const uint8_t* latches);
+
 int gbx_buffer(gbx_ctx* ctx, int32_t which, void** dev_ptr, int64_t* nbytes);
 int gbx_info(gbx_ctx* ctx, int32_t key, int64_t* out);
 

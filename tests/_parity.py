@@ -44,3 +44,35 @@ def assert_same_state(dut, ref, *, step: int, tag: str, mem: bool = True) -> Non
                 f"[{tag} step {step}] memory differs in {len(bad)} bytes; first env {e} "
                 f"addr {a:#06x}: hip={got[e, a]:#04x} oracle={ref.mem[e, a]:#04x}"
             )
+
+
+def ref_export_env(ref, env: int):
+    """The oracle's env ``env`` as an ``EnvImage`` (what ``gbx_export_env``
+    returns for the HIP backend)."""
+    from gbxcule_amd.abi import parse_cartridge_header
+    from gbxcule_amd.state_io import FIELDS, EnvImage
+
+    # a cart without RAM still has a 1-byte dummy slot per env in the oracle
+    ram = parse_cartridge_header(ref._rom.tobytes()).ram_byte_length
+    return EnvImage(
+        scalars=np.array([int(ref.field(n)[env]) for n in FIELDS], dtype=np.int64),
+        cart_state=ref.cart_state[env].copy(),
+        mem=ref.mem[env].copy(),
+        cart_ram=ref.cart_ram[env, :ram].copy() if ram else np.zeros(0, np.uint8),
+    )
+
+
+def ref_import_env(ref, env: int, img) -> None:
+    """Write an ``EnvImage`` into the oracle, as ``gbx_import_env`` does on the
+    device (cart RAM and latches only when the image carries them)."""
+    from gbxcule_amd.state_io import FIELDS
+
+    for i, n in enumerate(FIELDS):
+        v = ref.field(n)
+        v[env] = np.array(img.scalars[i]).astype(v.dtype)
+    ref.cart_state[env] = img.cart_state
+    ref.mem[env] = img.mem
+    if img.cart_ram.size:
+        ref.cart_ram[env, : img.cart_ram.size] = img.cart_ram
+    if img.latches is not None:
+        ref.latches[:] = img.latches
