@@ -23,7 +23,7 @@ FIELDS = (
 )  # fmt: skip
 FIELD_ID = {name: i for i, name in enumerate(FIELDS)}
 
-BUF_MEM, BUF_PIX, BUF_PIX_PACKED, BUF_OBS, BUF_REWARD, BUF_ACTIONS, BUF_CART_RAM = range(7)
+BUF_MEM, BUF_PIX, BUF_PIX_PACKED, BUF_OBS, BUF_REWARD, BUF_ACTIONS, BUF_CART_RAM, BUF_FRAME_BG = range(8)
 (
     INFO_NUM_ENVS,
     INFO_PADDED_ENVS,
@@ -49,6 +49,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gbx_upload_actions": (ctypes.c_int, [_vp, _vp, _vp]),
     "gbx_step": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp]),
     "gbx_render": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
+    "gbx_render_bg_env0": (ctypes.c_int, [_vp, _vp, _vp]),
     "gbx_snapshot": (ctypes.c_int, [_vp, _i32, _i32, _vp]),
     "gbx_masked_reset": (ctypes.c_int, [_vp, _vp, _vp]),
     "gbx_gather_mem": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp]),

@@ -128,8 +128,6 @@ class HipVecBackend:
             raise ValueError(f"unknown stage {stage!r}")
         if num_envs <= 0:
             raise ValueError("num_envs must be > 0")
-        if render_bg:
-            raise NotImplementedError("the env-0 scanline renderer is not part of this build")
         _lib.load()
         self.num_envs = int(num_envs)
         self.device = "cuda"
@@ -140,6 +138,7 @@ class HipVecBackend:
         self._release_after_frames = int(release_after_frames)
         self._base_seed = base_seed
         self._stage = stage
+        self._render_bg = bool(render_bg)
         self._render_pixels = bool(render_pixels)
         self._render_pixels_packed = bool(render_pixels_packed)
         self._render_on_step = bool(render_on_step)
@@ -306,6 +305,8 @@ class HipVecBackend:
             STAGE_ID[self._stage],
             stream,
         )
+        if render and self._render_bg:
+            self._call("gbx_render_bg_env0", self.ctx, None, stream)
         if render and self._render_on_step:
             self._launch_render_pixels()
 
@@ -395,6 +396,21 @@ class HipVecBackend:
             0,
             ctypes.c_void_p(_cur_stream()),
         )
+
+    def read_frame_bg_shade_env0(self) -> bytes:
+        """Env 0's 160x144 frame of shades 0-3, rendered after each step when
+        ``render_bg`` is set (reference warp_vec.py:852-857, 1389-1407)."""
+        if not self._initialized:
+            raise RuntimeError("Backend not initialized. Call reset() first.")
+        return self.frame_bg_torch().cpu().numpy().tobytes()
+
+    def frame_bg_torch(self):
+        """Device view ``[144, 160]`` uint8 of env 0's latched full frame."""
+        return self._view(_lib.BUF_FRAME_BG, (144, 160), "uint8")
+
+    def render_bg_env0(self) -> None:
+        """Render env 0's full frame now, from the latches of its last step."""
+        self._call("gbx_render_bg_env0", self.ctx, None, ctypes.c_void_p(_cur_stream()))
 
     def pixels_torch(self):
         if not self._initialized or not self._render_pixels:

@@ -52,7 +52,7 @@ constexpr int kHashLen = kMemSize + 128;
 void free_ctx(gbx_ctx* c) {
   DevState& s = c->s;
   void* ptrs[] = {s.mem, s.cram, s.cs, s.sc, s.cnt, s.serial, s.actions, s.obs, s.reward,
-                  s.pix, s.pix_packed, s.latches, (void*)s.rom, (void*)s.boot, (void*)s.recs,
+                  s.pix, s.pix_packed, s.latches, s.frame_bg, (void*)s.rom, (void*)s.boot, (void*)s.recs,
                   c->snap.mem, c->snap.cram, c->snap.serial, c->snap.pix, c->snap.cs,
                   c->snap.sc, c->snap.cnt, c->hash_k};
   for (void* p : ptrs)
@@ -180,6 +180,7 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   A(dalloc(&s.pix, (size_t)num_envs * kDsW * kDsH));
   A(dalloc(&s.pix_packed, (size_t)num_envs * kDsWB * kDsH));
   A(dalloc(&s.latches, (size_t)9 * kScreenH));
+  A(dalloc(&s.frame_bg, (size_t)kScreenW * kScreenH));
   uint8_t *drom = nullptr, *dboot = nullptr;
   Rec* drecs = nullptr;
   A(dalloc(&drom, (size_t)(rom_bytes + 0x100 + kOpenBusBytes)));
@@ -247,6 +248,7 @@ int gbx_reset(gbx_ctx* ctx, void* stream) {
   HIP_TRY(hipMemsetAsync(s.pix, 0, (size_t)s.n * kDsW * kDsH, st));
   HIP_TRY(hipMemsetAsync(s.pix_packed, 0, (size_t)s.n * kDsWB * kDsH, st));
   HIP_TRY(hipMemsetAsync(s.latches, 0, 9 * kScreenH, st));
+  HIP_TRY(hipMemsetAsync(s.frame_bg, 0, (size_t)kScreenW * kScreenH, st));
   HIP_TRY(launch_reset(s, st));
   return GBX_OK;
 }
@@ -286,6 +288,13 @@ int gbx_render(gbx_ctx* ctx, uint8_t* out_dev, int64_t base_offset, int32_t pack
     out = packed ? ctx->s.pix_packed : ctx->s.pix;
   }
   HIP_TRY(launch_render(ctx->s, out, base_offset, packed ? 1 : 0, (hipStream_t)stream));
+  return GBX_OK;
+}
+
+int gbx_render_bg_env0(gbx_ctx* ctx, uint8_t* out_dev, void* stream) {
+  CHECK_CTX(ctx);
+  HIP_TRY(launch_render_bg_env0(ctx->s, out_dev ? out_dev : ctx->s.frame_bg,
+                                (hipStream_t)stream));
   return GBX_OK;
 }
 
@@ -530,6 +539,7 @@ int gbx_buffer(gbx_ctx* ctx, int32_t which, void** dev_ptr, int64_t* nbytes) {
     case GBX_BUF_MEM: *dev_ptr = s.mem; *nbytes = (int64_t)s.npad * kMemSize; break;
     case GBX_BUF_PIX: *dev_ptr = s.pix; *nbytes = (int64_t)s.n * kDsW * kDsH; break;
     case GBX_BUF_PIX_PACKED: *dev_ptr = s.pix_packed; *nbytes = (int64_t)s.n * kDsWB * kDsH; break;
+    case GBX_BUF_FRAME_BG: *dev_ptr = s.frame_bg; *nbytes = (int64_t)kScreenW * kScreenH; break;
     case GBX_BUF_OBS: *dev_ptr = s.obs; *nbytes = (int64_t)s.n * s.obs_dim * 4; break;
     case GBX_BUF_REWARD: *dev_ptr = s.reward; *nbytes = (int64_t)s.n * 4; break;
     case GBX_BUF_ACTIONS: *dev_ptr = s.actions; *nbytes = (int64_t)s.n * 4; break;

@@ -167,6 +167,103 @@ __global__ void render_kernel(DevState s, uint8_t* out, int64_t base, int packed
 }
 
 // ---------------------------------------------------------------------------
+// Env 0's full 160x144 frame from its scanline latches (reference
+// kernels/ppu_step.py:12-176): LCDC, SCX, SCY, BGP, WX, WY, the window line,
+// OBP0 and OBP1 of each line as the step captured them; VRAM and OAM as they
+// are now.  One workgroup per line.  Wavefront 0 selects the line's sprites
+// first (the first 10 OAM entries that overlap the line, counted before the
+// x test) with one ballot, into LDS in OAM order; then every thread renders
+// one pixel against at most those 10.
+// ---------------------------------------------------------------------------
+constexpr int kFrameThreads = 192;  // 160 pixels, three wavefronts
+
+__global__ __launch_bounds__(kFrameThreads) void frame_bg_kernel(DevState s, uint8_t* out) {
+  __shared__ uint32_t cand[10];
+  __shared__ uint32_t ncand;
+  const uint32_t y = blockIdx.x;
+  const uint32_t x = threadIdx.x;
+  const Row r{s.mem, 0u};  // env 0: block 0, lane 0
+  const uint8_t* L = s.latches;
+  const uint32_t lcdc = L[0 * kScreenH + y], scx = L[1 * kScreenH + y];
+  const uint32_t scy = L[2 * kScreenH + y], bgp = L[3 * kScreenH + y];
+  const uint32_t wx = L[4 * kScreenH + y], wy = L[5 * kScreenH + y];
+  const uint32_t win_line = L[6 * kScreenH + y];
+  const uint32_t obp0 = L[7 * kScreenH + y], obp1 = L[8 * kScreenH + y];
+  const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
+  if (x < 64u) {
+    bool on = false;
+    if (x < 40u && (lcdc & 0x02u)) {
+      const uint32_t sy = r.M(0xFE00u + 4u * x), sx = r.M(0xFE01u + 4u * x);
+      const int top = (int)sy - 16;
+      on = sx != 0 && sy != 0 && sx < 168u && sy < 160u && (int)y >= top &&
+           (int)y < top + (int)height;
+    }
+    const uint64_t mask = __ballot(on);
+    const uint32_t rank = (uint32_t)__builtin_popcountll(mask & ((1ull << x) - 1ull));
+    if (on && rank < 10u) cand[rank] = x;
+    if (x == 0) {
+      const uint32_t total = (uint32_t)__builtin_popcountll(mask);
+      ncand = total < 10u ? total : 10u;
+    }
+  }
+  __syncthreads();
+  if (x >= (uint32_t)kScreenW) return;
+
+  uint32_t shade = 0, bg_color = 0;
+  if (lcdc & 0x01u) {
+    uint32_t px, py, map;
+    if ((lcdc & 0x20u) && y >= wy && (int)x >= (int)wx - 7) {
+      px = (uint32_t)((int)x - ((int)wx - 7)) & 0xFFu;
+      py = win_line & 0xFFu;
+      map = (lcdc & 0x40u) ? 0x9C00u : 0x9800u;
+    } else {
+      px = (x + scx) & 0xFFu;
+      py = (y + scy) & 0xFFu;
+      map = (lcdc & 0x08u) ? 0x9C00u : 0x9800u;
+    }
+    const uint32_t tile_id = r.M(map + (py >> 3) * 32u + (px >> 3));
+    bg_color = tile_pixel(r, bg_tile_addr(lcdc, tile_id), py & 7u, 7u - (px & 7u));
+    shade = (bgp >> (bg_color * 2u)) & 3u;
+  }
+  const uint32_t nc = ncand;
+  bool found = false;
+  int best_x = 0;
+  uint32_t best_color = 0, best_attr = 0;
+  for (uint32_t c = 0; c < nc; ++c) {  // OAM order: an x tie keeps the lower index
+    const uint32_t k = cand[c];
+    const int left = (int)r.M(0xFE01u + 4u * k) - 8;
+    if ((int)x < left || (int)x >= left + 8) continue;
+    const int top = (int)r.M(0xFE00u + 4u * k) - 16;
+    uint32_t tile = r.M(0xFE02u + 4u * k);
+    const uint32_t attr = r.M(0xFE03u + 4u * k);
+    uint32_t row = (uint32_t)((int)y - top);
+    if ((attr >> 6) & 1u) row = height - 1u - row;
+    if (height == 16u) {
+      tile &= 0xFEu;
+      if (row >= 8u) {
+        tile += 1u;
+        row -= 8u;
+      }
+    }
+    const uint32_t pxl = (uint32_t)((int)x - left);
+    const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
+    const uint32_t color = tile_pixel(r, 0x8000u + tile * 16u, row, bit);
+    if (color == 0) continue;
+    if (!found || left < best_x) {
+      found = true;
+      best_x = left;
+      best_color = color;
+      best_attr = attr;
+    }
+  }
+  if (found && !(((best_attr >> 7) & 1u) && bg_color != 0)) {
+    const uint32_t pal = ((best_attr >> 4) & 1u) ? obp1 : obp0;
+    shade = (pal >> (best_color * 2u)) & 3u;
+  }
+  out[y * (uint32_t)kScreenW + x] = (uint8_t)shade;
+}
+
+// ---------------------------------------------------------------------------
 // Reset snapshot (core/reset_cache.py:68-190): one env into env-major buffers.
 // ---------------------------------------------------------------------------
 __global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int with_pix) {
@@ -328,6 +425,11 @@ hipError_t launch_reset(const DevState& s, hipStream_t st) {
                      reinterpret_cast<uint4*>(s.mem), n16, s.boot);
   hipLaunchKernelGGL(init_state_kernel, dim3((unsigned)((s.npad + 255) / 256)), dim3(256), 0, st,
                      s.cs, s.sc, s.npad, s.mbc_kind);
+  return hipGetLastError();
+}
+
+hipError_t launch_render_bg_env0(const DevState& s, uint8_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(frame_bg_kernel, dim3(kScreenH), dim3(kFrameThreads), 0, st, s, out);
   return hipGetLastError();
 }
 

@@ -14,6 +14,7 @@ constexpr int kSerialMax = 1024;
 constexpr int kCartStateStride = 20;
 constexpr int kScreenH = 144;
 constexpr int kDsW = 80, kDsH = 72, kDsWB = 20;
+constexpr int kScreenW = 160;
 constexpr int kNumFields = 32;
 
 // cart_state slots (reference core/cartridge.py:55-76)
@@ -80,6 +81,7 @@ struct DevState {
   uint8_t* pix;         // [n][72][80]
   uint8_t* pix_packed;  // [n][72][20]
   uint8_t* latches;     // [9][144] env-0 scanline latches
+  uint8_t* frame_bg;    // [144][160] env-0 full-frame shades
   const uint8_t* rom;       // ROM image, the 256-byte boot image, 16 KiB of 0xFF (open bus)
   const uint8_t* boot;
   const uint4* recs;        // pre-decoded instruction record per byte of the ROM buffer
@@ -99,5 +101,6 @@ hipError_t launch_step(const DevState& s, const StepArgs& a, hipStream_t st);
 hipError_t launch_render(const DevState& s, uint8_t* out, int64_t base, int packed,
                          hipStream_t st);
 hipError_t launch_reset(const DevState& s, hipStream_t st);
+hipError_t launch_render_bg_env0(const DevState& s, uint8_t* out, hipStream_t st);
 
 }  // namespace gbx

@@ -60,7 +60,8 @@ enum {
   GBX_BUF_OBS = 3,        /* f32 [N][obs_dim] */
   GBX_BUF_REWARD = 4,     /* f32 [N] */
   GBX_BUF_ACTIONS = 5,    /* i32 [N] internal action buffer */
-  GBX_BUF_CART_RAM = 6    /* u8, 64-env blocks: [(N+63)/64][ram_stride][64] */
+  GBX_BUF_CART_RAM = 6,   /* u8, 64-env blocks: [(N+63)/64][ram_stride][64] */
+  GBX_BUF_FRAME_BG = 7    /* u8 [144][160] env-0 frame shades (gbx_render_bg_env0) */
 };
 
 /* gbx_info keys. */
@@ -101,6 +102,12 @@ int gbx_step(gbx_ctx* ctx, const int32_t* actions_dev, int32_t frames_to_run,
  * pix_packed buffer; base_offset is in bytes. */
 int gbx_render(gbx_ctx* ctx, uint8_t* out_dev, int64_t base_offset,
                int32_t packed, void* stream);
+
+/* Env 0's full 160x144 frame of shades 0-3 from the scanline latches its
+ * last step captured (kernels/ppu_step.py:12-176, launched after cpu_step
+ * when render_bg is set, backends/warp_vec.py:651-670).  out_dev NULL
+ * selects the internal GBX_BUF_FRAME_BG buffer. */
+int gbx_render_bg_env0(gbx_ctx* ctx, uint8_t* out_dev, void* stream);
 
 /* Capture env_idx as the reset snapshot (ResetCache.from_backend,
  * core/reset_cache.py:68-190); with_pix also snapshots the pix buffer. */

@@ -1112,10 +1112,20 @@ void write_post_step(RefMachine& m, int i, int stage) {
   }
 }
 
-// kernels/ppu_render_downsampled.py:27-179
-int sample_shade(const uint8_t* mem, int x, int y) {
-  const int lcdc = mem[0xFF40], scy = mem[0xFF42], scx = mem[0xFF43], bgp = mem[0xFF47];
-  const int obp0 = mem[0xFF48], obp1 = mem[0xFF49], wy = mem[0xFF4A], wx = mem[0xFF4B];
+// Registers one shade lookup reads.  The snapshot renderer takes them from
+// the IO page at render time; the env-0 frame renderer from the per-line
+// latches captured during the step.
+struct LineRegs {
+  int lcdc, scx, scy, bgp, wx, wy, obp0, obp1;
+  int win_row;  // window tile-row line: y - WY (snapshot) or the latched window line
+};
+
+// Shade of pixel (x, y): background/window then sprites
+// (kernels/ppu_render_downsampled.py:27-179; kernels/ppu_step.py:12-171 is
+// the same rule with latched registers).
+int shade_at(const uint8_t* mem, int x, int y, const LineRegs& r) {
+  const int lcdc = r.lcdc, scy = r.scy, scx = r.scx, bgp = r.bgp;
+  const int obp0 = r.obp0, obp1 = r.obp1, wy = r.wy, wx = r.wx;
   int shade = 0, bg_color = 0;
   auto tile_row = [&](int tile_id, int row, bool unsigned_data) {
     int addr;
@@ -1128,7 +1138,7 @@ int sample_shade(const uint8_t* mem, int x, int y) {
     int map, px, py;
     if (use_window) {
       px = x - (wx - 7);
-      py = y - wy;
+      py = r.win_row;
       map = (lcdc & 0x40) ? 0x9C00 : 0x9800;
       px &= 0xFF;
       py &= 0xFF;
@@ -1185,6 +1195,21 @@ int sample_shade(const uint8_t* mem, int x, int y) {
     }
   }
   return shade;
+}
+
+// kernels/ppu_render_downsampled.py:27-179: registers from the IO page
+int sample_shade(const uint8_t* mem, int x, int y) {
+  LineRegs r;
+  r.lcdc = mem[0xFF40];
+  r.scy = mem[0xFF42];
+  r.scx = mem[0xFF43];
+  r.bgp = mem[0xFF47];
+  r.obp0 = mem[0xFF48];
+  r.obp1 = mem[0xFF49];
+  r.wy = mem[0xFF4A];
+  r.wx = mem[0xFF4B];
+  r.win_row = y - r.wy;
+  return shade_at(mem, x, y, r);
 }
 
 }  // namespace
@@ -1313,6 +1338,28 @@ int ref_render(RefMachine* m, int packed, int nthreads) {
               (uint8_t)sample_shade(mem, ox * 2, oy * 2);
       }
     }
+  }
+  return 0;
+}
+
+// kernels/ppu_step.py:12-176: env 0's full 160x144 frame from the per-line
+// latches (LCDC, SCX, SCY, BGP, WX, WY, window line, OBP0, OBP1) and the
+// current VRAM/OAM of env 0.
+int ref_render_bg_env0(RefMachine* m, uint8_t* out) {
+  if (!m || !out || m->n <= 0) return -1;
+  const uint8_t* mem = &m->mem[0];
+  for (int y = 0; y < SCREEN_H; ++y) {
+    LineRegs r;
+    r.lcdc = m->latches[0][y];
+    r.scx = m->latches[1][y];
+    r.scy = m->latches[2][y];
+    r.bgp = m->latches[3][y];
+    r.wx = m->latches[4][y];
+    r.wy = m->latches[5][y];
+    r.win_row = m->latches[6][y];
+    r.obp0 = m->latches[7][y];
+    r.obp1 = m->latches[8][y];
+    for (int x = 0; x < 160; ++x) out[y * 160 + x] = (uint8_t)shade_at(mem, x, y, r);
   }
   return 0;
 }

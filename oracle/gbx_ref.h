@@ -47,6 +47,8 @@ int ref_step(RefMachine* m, const int32_t* actions, int frames_to_run,
              int nthreads);
 /* Snapshot renderer into the machine's pix (packed=0) or pix_packed buffer. */
 int ref_render(RefMachine* m, int packed, int nthreads);
+/* Env 0's 160x144 shade frame from its scanline latches (kernels/ppu_step.py). */
+int ref_render_bg_env0(RefMachine* m, uint8_t* out);
 int ref_snapshot(RefMachine* m, int env_idx);
 int ref_masked_reset(RefMachine* m, const uint8_t* mask);
 void* ref_field_ptr(RefMachine* m, int field, int64_t* nbytes, int* elem_size);

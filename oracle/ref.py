@@ -55,6 +55,7 @@ def load() -> ctypes.CDLL:
         lib.ref_reset.argtypes = [vp]
         lib.ref_step.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32]
         lib.ref_render.argtypes = [vp, i32, i32]
+        lib.ref_render_bg_env0.argtypes = [vp, vp]
         lib.ref_snapshot_ex.argtypes = [vp, i32, i32]
         lib.ref_masked_reset.argtypes = [vp, vp]
         lib.ref_set_debug.argtypes = [vp, i32, i32, i32, i32]
@@ -188,6 +189,13 @@ class RefMachine:
 
     def render(self, packed: bool, threads: int = 1) -> None:
         self._lib.ref_render(self._h, 1 if packed else 0, threads)
+
+    def render_bg_env0(self) -> np.ndarray:
+        """Env 0's 160x144 shade frame from its scanline latches."""
+        out = np.zeros((144, 160), dtype=np.uint8)
+        if self._lib.ref_render_bg_env0(self._h, out.ctypes.data) != 0:
+            raise RuntimeError("ref_render_bg_env0 failed")
+        return out
 
     def snapshot(self, env_idx: int = 0, with_pix: bool = False) -> None:
         if self._lib.ref_snapshot_ex(self._h, env_idx, 1 if with_pix else 0) != 0:

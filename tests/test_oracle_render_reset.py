@@ -31,18 +31,20 @@ def unpack(packed: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
-# independent full-frame renderer (160x144), then sampled at even x/y
+# independent full-frame renderer (160x144), one line at a time with that
+# line's registers: from the IO page (snapshot renderer, then sampled at even
+# x/y) or from the env-0 scanline latches (full-frame renderer)
 # ---------------------------------------------------------------------------
-def frame_np(mem: np.ndarray) -> np.ndarray:
-    lcdc, scy, scx, bgp = (int(mem[a]) for a in (0xFF40, 0xFF42, 0xFF43, 0xFF47))
-    obp = (int(mem[0xFF48]), int(mem[0xFF49]))
-    wy, wx = int(mem[0xFF4A]), int(mem[0xFF4B])
-    ys, xs = np.mgrid[0:144, 0:160]
-    color = np.zeros((144, 160), np.int64)
+def line_np(mem: np.ndarray, y: int, regs: dict) -> np.ndarray:
+    lcdc, scy, scx, bgp = regs["lcdc"], regs["scy"], regs["scx"], regs["bgp"]
+    obp = (regs["obp0"], regs["obp1"])
+    wy, wx, win_row = regs["wy"], regs["wx"], regs["win_row"]
+    xs = np.arange(160)
+    color = np.zeros(160, np.int64)
     if lcdc & 1:
-        win = bool(lcdc & 0x20) & (ys >= wy) & (xs >= wx - 7)
+        win = bool(lcdc & 0x20) & (y >= wy) & (xs >= wx - 7)
         px = np.where(win, (xs - (wx - 7)) & 0xFF, (xs + scx) & 0xFF)
-        py = np.where(win, (ys - wy) & 0xFF, (ys + scy) & 0xFF)
+        py = np.where(win, win_row & 0xFF, (y + scy) & 0xFF)
         mapbase = np.where(win, 0x9C00 if lcdc & 0x40 else 0x9800, 0x9C00 if lcdc & 0x08 else 0x9800)
         tid = mem[mapbase + (py // 8) * 32 + px // 8].astype(np.int64)
         if lcdc & 0x10:
@@ -57,35 +59,51 @@ def frame_np(mem: np.ndarray) -> np.ndarray:
     if lcdc & 2:
         h = 16 if lcdc & 4 else 8
         oam = mem[0xFE00:0xFEA0].reshape(40, 4).astype(np.int64)
-        for y in range(144):
-            line = [
-                k for k in range(40)
-                if 0 < oam[k, 1] < 168 and 0 < oam[k, 0] < 160 and oam[k, 0] - 16 <= y < oam[k, 0] - 16 + h
-            ][:10]  # fmt: skip
-            best = {}
-            for k in line:
-                sy, sx, tile, attr = oam[k]
-                row = y - (sy - 16)
-                if attr & 0x40:
-                    row = h - 1 - row
-                if h == 16:
-                    tile = (tile & 0xFE) + (1 if row >= 8 else 0)
-                    row %= 8
-                lo = int(mem[0x8000 + tile * 16 + row * 2])
-                hi = int(mem[0x8000 + tile * 16 + row * 2 + 1])
-                for x in range(max(sx - 8, 0), min(sx, 160)):
-                    p = x - (sx - 8)
-                    b = p if attr & 0x20 else 7 - p
-                    c = ((hi >> b) & 1) * 2 + ((lo >> b) & 1)
-                    if c == 0:
-                        continue
-                    if x not in best or sx - 8 < best[x][0]:
-                        best[x] = (sx - 8, c, attr)
-            for x, (_, c, attr) in best.items():
-                if attr & 0x80 and lcdc & 1 and color[y, x] != 0:
+        line = [
+            k for k in range(40)
+            if 0 < oam[k, 1] < 168 and 0 < oam[k, 0] < 160 and oam[k, 0] - 16 <= y < oam[k, 0] - 16 + h
+        ][:10]  # fmt: skip
+        best = {}
+        for k in line:
+            sy, sx, tile, attr = oam[k]
+            row = y - (sy - 16)
+            if attr & 0x40:
+                row = h - 1 - row
+            if h == 16:
+                tile = (tile & 0xFE) + (1 if row >= 8 else 0)
+                row %= 8
+            lo = int(mem[0x8000 + tile * 16 + row * 2])
+            hi = int(mem[0x8000 + tile * 16 + row * 2 + 1])
+            for x in range(max(sx - 8, 0), min(sx, 160)):
+                p = x - (sx - 8)
+                b = p if attr & 0x20 else 7 - p
+                c = ((hi >> b) & 1) * 2 + ((lo >> b) & 1)
+                if c == 0:
                     continue
-                shade[y, x] = (obp[(attr >> 4) & 1] >> (2 * c)) & 3
+                if x not in best or sx - 8 < best[x][0]:
+                    best[x] = (sx - 8, c, attr)
+        for x, (_, c, attr) in best.items():
+            if attr & 0x80 and lcdc & 1 and color[x] != 0:
+                continue
+            shade[x] = (obp[(attr >> 4) & 1] >> (2 * c)) & 3
     return shade.astype(np.uint8)
+
+
+def frame_np(mem: np.ndarray) -> np.ndarray:
+    r = {k: int(mem[a]) for k, a in (("lcdc", 0xFF40), ("scy", 0xFF42), ("scx", 0xFF43),
+                                     ("bgp", 0xFF47), ("obp0", 0xFF48), ("obp1", 0xFF49),
+                                     ("wy", 0xFF4A), ("wx", 0xFF4B))}  # fmt: skip
+    return np.stack([line_np(mem, y, dict(r, win_row=y - r["wy"])) for y in range(144)])
+
+
+LATCH_ROWS = ("lcdc", "scx", "scy", "bgp", "wx", "wy", "win_row", "obp0", "obp1")
+
+
+def frame_latched_np(mem: np.ndarray, lat: np.ndarray) -> np.ndarray:
+    rows = []
+    for y in range(144):
+        rows.append(line_np(mem, y, {k: int(lat[i, y]) for i, k in enumerate(LATCH_ROWS)}))
+    return np.stack(rows)
 
 
 def render_both(m):
@@ -268,5 +286,90 @@ def test_idle_run_keeps_frame_counter_consistent():
         cyc = m.field("cycle_count")
         assert (cyc >= 3 * 70224).all() and (cyc < 3 * 70224 + 12).all()
         np.testing.assert_array_equal(m.field("cycle_in_frame"), cyc - 3 * 70224)
+    finally:
+        m.close()
+
+
+# ---------------------------------------------------------------------------
+# env-0 full-frame renderer from the scanline latches (kernels/ppu_step.py)
+# ---------------------------------------------------------------------------
+def test_env0_frame_matches_independent_latched_renderer():
+    """Random VRAM/OAM and random per-line latches (every register different
+    on every line), against the line-by-line numpy renderer."""
+    rng = np.random.default_rng(21)
+    m = _idle(1)
+    try:
+        for trial in range(12):
+            m.mem[0, 0x8000:0xA000] = rng.integers(0, 256, 0x2000)
+            oam = rng.integers(0, 256, 160)
+            oam[0::4] = rng.integers(0, 176, 40)
+            oam[1::4] = rng.integers(0, 176, 40)
+            m.mem[0, 0xFE00:0xFEA0] = oam
+            lat = rng.integers(0, 256, (9, 144)).astype(np.uint8)
+            lat[5] = rng.integers(0, 160, 144)  # WY mostly on screen
+            lat[4] = rng.integers(0, 175, 144)
+            if trial % 3 == 0:
+                lat[0] = rng.integers(0, 256)  # one LCDC for the whole frame
+            m.latches[:] = lat
+            got = m.render_bg_env0()
+            want = frame_latched_np(m.mem[0], lat)
+            np.testing.assert_array_equal(got, want, err_msg=f"trial {trial}")
+    finally:
+        m.close()
+
+
+def test_env0_frame_with_steady_latches_equals_snapshot_renderer():
+    """Latches equal to the IO registers on every line (window line y - WY):
+    the full frame sampled at even x/y is exactly the snapshot render."""
+    rng = np.random.default_rng(22)
+    m = _idle(1)
+    try:
+        for trial in range(8):
+            mem = m.mem
+            mem[0, 0x8000:0xA000] = rng.integers(0, 256, 0x2000)
+            oam = rng.integers(0, 256, 160)
+            oam[0::4] = rng.integers(0, 176, 40)
+            oam[1::4] = rng.integers(0, 176, 40)
+            mem[0, 0xFE00:0xFEA0] = oam
+            for reg in (0xFF40, 0xFF42, 0xFF43, 0xFF47, 0xFF48, 0xFF49):
+                mem[0, reg] = rng.integers(0, 256)
+            mem[0, 0xFF4A], mem[0, 0xFF4B] = rng.integers(0, 144), rng.integers(0, 168)
+            ys = np.arange(144)
+            regs = [mem[0, a] for a in (0xFF40, 0xFF43, 0xFF42, 0xFF47, 0xFF4B, 0xFF4A)]
+            lat = np.zeros((9, 144), np.uint8)
+            lat[:6] = np.array(regs, np.uint8)[:, None]
+            lat[6] = np.where(ys >= mem[0, 0xFF4A], (ys - int(mem[0, 0xFF4A])) & 0xFF, 0)
+            lat[7], lat[8] = mem[0, 0xFF48], mem[0, 0xFF49]
+            m.latches[:] = lat
+            m.render(packed=False)
+            np.testing.assert_array_equal(m.render_bg_env0()[::2, ::2], m.pix[0])
+    finally:
+        m.close()
+
+
+def test_env0_frame_raster_scroll_known_answer():
+    """A per-line SCX latch (a raster effect): tile 1 lights only its leftmost
+    column, the map is all tile 1, and line y scrolls by y, so pixel (x, y) is
+    shade 3 exactly when (x + y) % 8 == 0; line 7 also switches to the window
+    (WX 7 + 40, window line 3) on the 9C00 map of tile 2 (all colour 2)."""
+    m = _idle(1)
+    mem = m.mem
+    try:
+        mem[0, 0x9800:0x9C00] = 1
+        mem[0, 0x9C00:0xA000] = 2
+        mem[0, 0x8010:0x8020] = [0x80, 0x80] * 8  # colour 3 at column 0
+        mem[0, 0x8020:0x8030] = [0x00, 0xFF] * 8  # colour 2 everywhere
+        lat = np.zeros((9, 144), np.uint8)
+        lat[0] = 0x91  # BG on, unsigned tiles, window off
+        lat[1] = np.arange(144) & 0xFF  # SCX = y
+        lat[3] = 0xE4
+        lat[0, 7] = 0xF1  # window on, map 9C00
+        lat[4, 7], lat[5, 7], lat[6, 7] = 7 + 40, 0, 3
+        m.latches[:] = lat
+        f = m.render_bg_env0()
+        ys, xs = np.mgrid[0:144, 0:160]
+        want = np.where((xs + ys) % 8 == 0, 3, 0)
+        want[7, 40:] = 2
+        np.testing.assert_array_equal(f, want)
     finally:
         m.close()
