@@ -110,6 +110,7 @@ __device__ __forceinline__ T* in_vgpr(T* p) {
 // ---------------------------------------------------------------------------
 struct Lane {
   const DevState& s;
+  int mbc;        // cartridge kind; a compile-time constant of each kernel variant
   uint32_t e;     // env index
   uint32_t lane;  // e % 64: position inside the 64-env block
   rsrc_t rm, rsc, rcs;             // memory image, scalars, cartridge state of the block
@@ -170,7 +171,7 @@ struct Lane {
     return bank % count;
   }
   __device__ void refresh_cart() {
-    const int kind = s.mbc_kind;
+    const int kind = mbc;
     const int lo_raw = CS(CS_ROM_BANK_LO);
     const int lo = lo_raw & 0x1F, hi = CS(CS_ROM_BANK_HI) & 3;
     const int mode = CS(CS_BANK_MODE) & 1;
@@ -350,7 +351,7 @@ struct Lane {
     rtc_dirty = 0;
   }
   __device__ void rtc_tick(int cycles) {
-    if (cycles <= 0 || s.mbc_kind != MBC_MBC3 || rtc_halt) return;
+    if (cycles <= 0 || mbc != MBC_MBC3 || rtc_halt) return;
     if (rtc_sub < 0) rtc_sub = 0;
     rtc_sub += cycles;
     if (rtc_sub >= kRtcCyclesPerSecond || rtc_dirty) rtc_slow();
@@ -461,7 +462,7 @@ struct Lane {
     }
   }
   __device__ void mbc_write(uint32_t x, uint32_t v) {
-    const int kind = s.mbc_kind;
+    const int kind = mbc;
     if (kind == MBC_MBC1) {
       if (x < 0x2000u) CS(CS_RAM_ENABLE) = (v & 0x0Fu) == 0x0Au ? 1 : 0;
       else if (x < 0x4000u) CS(CS_ROM_BANK_LO) = (v & 0x1Fu) ? (int)(v & 0x1Fu) : 1;
@@ -651,10 +652,14 @@ struct Lane {
 // ---------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------
+// One variant per cartridge kind (kMbc) and per debug mode (kDbg): the
+// cartridge code of other kinds and every debug check compile out.
+template <int kMbc, bool kDbg>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void step_kernel(DevState s, StepArgs args) {
   const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (uint32_t)s.n) return;
   Lane L{s};
+  L.mbc = kMbc;
   L.e = e;
   L.lane = e & (kEnvBlock - 1);
   const uint32_t blk = __builtin_amdgcn_readfirstlane(e >> kEnvBlockShift);
@@ -742,7 +747,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   };
   const uint32_t watch_val = dbg_watch ? watch_read() : 0u;
   const int frames = (int)in_vgpr((uint32_t)args.frames);
-  const bool dbg = args.dbg_rst38 || args.dbg_trap_pc || args.dbg_max_instr > 0 || args.dbg_watch;
+  constexpr bool dbg = kDbg;
 
   // record of the instruction at pc (valid when rv)
   uint4 rec = uint4{0u, 0u, 0u, 0u};
@@ -1011,7 +1016,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   L.M(0xFF45) = L.lyc;
   L.M(0xFF4A) = L.wy;
   L.M(0xFFFF) = L.ie;
-  if (s.mbc_kind == MBC_MBC3) L.CS(CS_RTC_LAST_CYCLE) = L.rtc_sub;
+  if (kMbc == MBC_MBC3) L.CS(CS_RTC_LAST_CYCLE) = L.rtc_sub;
 }
 
 }  // namespace
@@ -1022,7 +1027,16 @@ hipError_t launch_step(const DevState& s, const StepArgs& a, hipStream_t st) {
   // 64-env memory block, so a wavefront never straddles two blocks).
   const int threads = s.step_lanes;
   const int blocks = (s.n + threads - 1) / threads;
-  hipLaunchKernelGGL(step_kernel, dim3(blocks), dim3(threads), 0, st, s, a);
+  const bool dbg = a.dbg_rst38 || a.dbg_trap_pc || a.dbg_max_instr > 0 || a.dbg_watch;
+  const dim3 g(blocks), b(threads);
+  switch (s.mbc_kind * 2 + (dbg ? 1 : 0)) {
+    case MBC_ROM_ONLY * 2: hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, false>), g, b, 0, st, s, a); break;
+    case MBC_ROM_ONLY * 2 + 1: hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, true>), g, b, 0, st, s, a); break;
+    case MBC_MBC1 * 2: hipLaunchKernelGGL((step_kernel<MBC_MBC1, false>), g, b, 0, st, s, a); break;
+    case MBC_MBC1 * 2 + 1: hipLaunchKernelGGL((step_kernel<MBC_MBC1, true>), g, b, 0, st, s, a); break;
+    case MBC_MBC3 * 2: hipLaunchKernelGGL((step_kernel<MBC_MBC3, false>), g, b, 0, st, s, a); break;
+    default: hipLaunchKernelGGL((step_kernel<MBC_MBC3, true>), g, b, 0, st, s, a); break;
+  }
   return hipGetLastError();
 }
 
