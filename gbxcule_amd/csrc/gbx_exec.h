@@ -82,10 +82,13 @@ __device__ __forceinline__ ExecOut exec_insn(const ExecIn& in) {
   const uint32_t rs = (((hi << 8) | lo) >> ((r1 >> 22) & 7u)) & 0xFFu;
   const uint32_t cs = (xv >> ((r1 >> 25) & 15u)) & 1u;
 
+  // unit outputs picked with masks (every arm is computed above)
   const uint32_t unit = (r1 >> 12) & 3u;
-  uint32_t res = unit == U_ADD ? s9 & 0xFFu : unit == U_SHIFT ? rs : rl;
-  uint32_t hcomp = unit == U_ADD ? ((h5 >> 4) ^ sub) & 1u : 0u;
-  uint32_t ccomp = unit == U_ADD ? ((s9 >> 8) ^ sub) & 1u : unit == U_SHIFT ? cs : 0u;
+  const uint32_t madd = 0u - (uint32_t)(unit == U_ADD), msh = 0u - (uint32_t)(unit == U_SHIFT);
+  const uint32_t radd = s9 & 0xFFu, hadd = ((h5 >> 4) ^ sub) & 1u, cadd = ((s9 >> 8) ^ sub) & 1u;
+  uint32_t res = (radd & madd) | (rs & msh) | (rl & ~(madd | msh));
+  uint32_t hcomp = hadd & madd;
+  uint32_t ccomp = (cadd & madd) | (cs & msh);
   if (r1 >> 31) {  // DAA (alu.py:897-950)
     const uint32_t nf = (fl >> 6) & 1u, hf = (fl >> 5) & 1u;
     const bool dlo = nf ? hf != 0u : (hf != 0u || (xv & 15u) > 9u);
@@ -102,7 +105,10 @@ __device__ __forceinline__ ExecOut exec_insn(const ExecIn& in) {
   const uint32_t rsel = rr == 0u ? 0x0C0C0302u : rr == 1u ? 0x0C0C0100u
                         : rr == 2u ? 0x0C0C0706u : 0x0C0C040Cu;
   uint32_t rrv = __builtin_amdgcn_perm(in.w1, in.w0, rsel);
-  rrv = ((r3 >> 22) & 1u) ? rrv | fl : (rr == 3u ? sp : rrv);  // AF or SP
+  // pair 3 is AF (record bit 22: A from the perm, F or'ed in) or SP
+  const uint32_t maf = 0u - ((r3 >> 22) & 1u);
+  const uint32_t msp = (0u - (uint32_t)(rr == 3u)) & ~maf;
+  rrv = (rrv & ~msp) | (sp & msp) | (fl & maf);
   const uint32_t a16 = (r3 >> 8) & 3u, b16 = (r3 >> 12) & 7u;
   uint32_t A16 = a16 == 1u ? rrv : a16 == 2u ? hl : a16 == 3u ? sp : 0u;
   const uint32_t rd16 = in.rd0 | (in.rd1 << 8);
@@ -140,41 +146,39 @@ __device__ __forceinline__ ExecOut exec_insn(const ExecIn& in) {
   const uint32_t op16 = (r3 >> 4) & 15u, cc = (r3 >> 28) & 7u;
   const uint32_t cbit = cc <= 2u ? (fl >> 7) & 1u : (fl >> 4) & 1u;
   const bool is_jump = op16 - O_JR <= (uint32_t)(O_RST - O_JR);
-  const bool taken = !is_jump || cc == 0u || cbit == (uint32_t)((cc & 1u) == 0u);
+  const bool taken = (!is_jump) | (cc == 0u) | (cbit == (uint32_t)((cc & 1u) == 0u));
   const uint32_t seq = (in.pc + ((r0 >> 24) & 3u)) & 0xFFFFu;
   uint32_t target = imm16;  // JP, CALL
   target = op16 == O_JR ? (in.pc + 2u + sext8(b1)) & 0xFFFFu : target;
   target = op16 == O_JPHL ? hl : target;
-  target = (op16 == O_RET || op16 == O_RETI) ? rd16 : target;
+  target = ((op16 == O_RET) | (op16 == O_RETI)) ? rd16 : target;
   target = op16 == O_RST ? op & 0x38u : target;
   const bool trap = op16 == O_TRAP;
-  uint32_t npc = (is_jump && taken) ? target : seq;
+  uint32_t npc = (is_jump & taken) ? target : seq;
   o.npc = trap ? in.pc : npc;
   o.cycles = (taken ? (r0 >> 26) & 7u : r0 >> 29) << 2;
 
-  const bool push = op16 == O_PUSH || ((op16 == O_CALL || op16 == O_RST) && taken);
+  const bool push = (op16 == O_PUSH) | (((op16 == O_CALL) | (op16 == O_RST)) & taken);
   const uint32_t pushv = op16 == O_PUSH ? rrv : seq;
   const bool stsp = op16 == O_STSP;
-  if (r3 & 1u) {  // 8-bit result to the bus operand
-    o.wn = 1;
-    o.wa0 = in.ra;
-    o.wv0 = res;
-  }
-  if (push || stsp) {
-    o.wn = 2;
-    o.wa0 = stsp ? imm16 : (sp - 1u) & 0xFFFFu;
-    o.wv0 = stsp ? sp & 0xFFu : pushv >> 8;
-    o.wa1 = stsp ? (imm16 + 1u) & 0xFFFFu : (sp - 2u) & 0xFFFFu;
-    o.wv1 = stsp ? (sp >> 8) & 0xFFu : pushv & 0xFFu;
-  }
+  // bus writes as selects: an 8-bit result to the operand, or two bytes
+  // (PUSH / CALL / RST / LD (a16),SP)
+  const bool w16 = push | stsp;
+  const uint32_t wa0_16 = stsp ? imm16 : (sp - 1u) & 0xFFFFu;
+  const uint32_t wv0_16 = stsp ? sp & 0xFFu : pushv >> 8;
+  o.wn = w16 ? 2u : (r3 & 1u);
+  o.wa0 = w16 ? wa0_16 : in.ra;
+  o.wv0 = w16 ? wv0_16 : res;
+  o.wa1 = stsp ? (imm16 + 1u) & 0xFFFFu : (sp - 2u) & 0xFFFFu;
+  o.wv1 = stsp ? (sp >> 8) & 0xFFu : pushv & 0xFFu;
   uint32_t nsp = sp;
   nsp = push ? (sp - 2u) & 0xFFFFu : nsp;
-  nsp = (op16 == O_POP || ((op16 == O_RET || op16 == O_RETI) && taken)) ? (sp + 2u) & 0xFFFFu
-                                                                          : nsp;
+  const uint32_t sp_inc = (sp + 2u) & 0xFFFFu;
+  nsp = ((op16 == O_POP) | (((op16 == O_RET) | (op16 == O_RETI)) & taken)) ? sp_inc : nsp;
   nsp = ((r3 >> 15) & 1u) ? v16 : nsp;
   o.sp = nsp;
-  o.ime_on = (op16 == O_EI || op16 == O_RETI) ? 1u : 0u;
-  o.ime_set = (o.ime_on || op16 == O_DI) ? 1u : 0u;
+  o.ime_on = ((op16 == O_EI) | (op16 == O_RETI)) ? 1u : 0u;
+  o.ime_set = (o.ime_on | (uint32_t)(op16 == O_DI));
   o.halt = op16 == O_HALT ? 1u : 0u;
   o.trap = trap ? 1u : 0u;
   return o;

@@ -226,8 +226,10 @@ struct Lane {
   __device__ const uint8_t* bus_ptr(uint32_t x) const {
     const bool rom = x < 0x8000u;
     const bool cart = x - 0xA000u < 0x2000u;
-    const uint32_t roff = (boot_en && x < 0x100u) ? rom_len + x
-                                                   : (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
+    // bitwise conditions throughout the per-instruction path: each is a
+    // select, never a branch
+    const bool bootw = (boot_en != 0u) & (x < 0x100u);
+    const uint32_t roff = bootw ? rom_len + x : (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
     const uint32_t coff = ram_ok ? ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane : lane;
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
     p = cart ? cramb + coff : p;
@@ -294,7 +296,7 @@ struct Lane {
   __device__ void timer_tick(int cycles) {
     if (cycles <= 0) return;
     uint32_t d = div & 0xFFFFu;
-    if (!pend && (d & tmask) + (uint32_t)cycles <= tmask) {
+    if ((pend == 0u) & ((d & tmask) + (uint32_t)cycles <= tmask)) {
       d = (d + (uint32_t)cycles) & 0xFFFFu;  // no edge, no reload: DIV only
     } else {
       int rem = cycles;
@@ -381,7 +383,7 @@ struct Lane {
   __device__ static bool io_special(uint32_t x) {
     const uint32_t k = x & 0xFFu;
     const uint32_t m = k < 32u ? 0x80F5u : (k - 64u < 32u ? 0x10473u : 0u);
-    return x >= 0xFF00u && (k == 0xFFu || ((m >> (k & 31u)) & 1u));
+    return (x >= 0xFF00u) & ((k == 0xFFu) | (((m >> (k & 31u)) & 1u) != 0u));
   }
   __device__ void io_write(uint32_t x, uint32_t v) {
     const uint32_t k = x & 0xFFu;
@@ -512,7 +514,7 @@ struct Lane {
   }
   __device__ void write8(uint32_t addr, uint32_t v) {
     const uint32_t x = fold(addr);
-    const bool special = x < 0x8000u || x - 0xA000u < 0x2000u || io_special(x);
+    const bool special = (x < 0x8000u) | (x - 0xA000u < 0x2000u) | io_special(x);
     if (!special) M(x) = v;
     else write_special(x, v);
   }
@@ -633,11 +635,11 @@ struct Lane {
   // A pre-decoded record serves pc when all three instruction bytes lie in
   // one 16 KiB ROM window of a mapped bank, or in the boot image.
   __device__ bool rec_ok(uint32_t p) const {
-    if (boot_en && p < 0x100u) return p < 0xFEu;
-    return p < 0x8000u && (p & 0x3FFFu) <= 0x3FFDu;
+    const bool bw = (boot_en != 0u) & (p < 0x100u);
+    return (bw & (p < 0xFEu)) | (!bw & (p < 0x8000u) & ((p & 0x3FFFu) <= 0x3FFDu));
   }
   __device__ uint32_t rec_index(uint32_t p) const {
-    return (boot_en && p < 0x100u) ? rom_len + p
+    return ((boot_en != 0u) & (p < 0x100u)) ? rom_len + p
                                    : (p < 0x4000u ? rom_lo : rom_hi) + (p & 0x3FFFu);
   }
   // Fetch + decode through the bus (code in RAM, window edges, open bus).
@@ -755,7 +757,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
 
   // One exit: the frame count reached or the env trapped (a trap freezes
   // the env for the rest of the launch, misc.py:42-56).
-  while (L.frames_done < frames && !trap) {
+  while ((L.frames_done < frames) & (trap == 0)) {
     const uint32_t lcdc_prev = L.lcdc & 0x80u;
     const bool hiter = L.halted != 0;
     int cycles = 4;
@@ -807,7 +809,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
         if (nr > 1u) {
           x1 = Lane::fold(in.ra + 1u);
           p1 = p0 + kEnvBlock;
-          if (x1 != x0 + 1u || x0 < 0x8000u || x0 - 0xA000u < 0x2000u || x1 - 0xA000u < 0x2000u)
+          if ((x1 != x0 + 1u) | (x0 < 0x8000u) | (x0 - 0xA000u < 0x2000u) | (x1 - 0xA000u < 0x2000u))
             p1 = L.bus_ptr(x1);
         }
         const uint32_t v0 = *p0, v1 = *p1;
@@ -830,7 +832,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       L.ime = o.ime_set ? o.ime_on : L.ime;
       L.ime_delay = o.ime_set ? 0u : L.ime_delay;
       L.halted = o.halt ? 1u : L.halted;
-      if (o.trap && !trap) {  // misc.py:42-56: freeze the env, pc unchanged
+      if ((o.trap != 0u) & (trap == 0)) {  // misc.py:42-56: freeze the env, pc unchanged
         trap = 1;
         trap_pc = (int)pc;
         trap_op = (int)op;
@@ -866,7 +868,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     }
     if (!trap) {
       L.timer_tick(cycles);
-      if (!hiter && L.ime_delay) {
+      if (!hiter & (L.ime_delay != 0u)) {
         L.ime = 1;
         L.ime_delay = 0;
       }
@@ -904,7 +906,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       L.rtc_tick(total);
       ncyc += (uint32_t)total;
       cframe += total;
-      if (((lcdc_prev ^ lcdc_now) & 0x80u) || cframe >= kCyclesPerFrame) {
+      if ((((lcdc_prev ^ lcdc_now) & 0x80u) != 0u) | (cframe >= kCyclesPerFrame)) {
         // LCD toggles and frame ends (cpu_step_builder.py frame loop)
         instr += ninstr;
         cyc += ncyc;
