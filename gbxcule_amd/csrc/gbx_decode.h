@@ -1,377 +1,471 @@
-// gbx_decode.h -- SM83 instruction decode into a 128-bit micro-op record.
+// gbx_decode.h -- SM83 instruction decode into a 512-bit micro-op record.
 //
 // Every instruction (unprefixed opcode, or CB prefix + second byte) maps to
-// one record of four 32-bit words whose fields drive the step kernel's
-// straight-line datapath.  Cycle counts, lengths and operand roles follow
-// the reference opcode table (src/gbxcule/core/isa_sm83.py) and the opcode
-// templates under src/gbxcule/kernels/cpu_templates/ (loads.py, alu.py,
-// bitops.py, jumps.py, stack.py, misc.py).
+// one record of sixteen 32-bit words that drive the step kernel's
+// straight-line datapath (gbx_exec.h).  Cycle counts, lengths and operand
+// roles follow the reference opcode table (src/gbxcule/core/isa_sm83.py)
+// and the opcode templates under src/gbxcule/kernels/cpu_templates/
+// (loads.py, alu.py, bitops.py, jumps.py, stack.py, misc.py).
 //
-// Register file.  The eight 8-bit registers live in two dwords read and
-// written with byte permutes: w0 = B C D E (B in bits 31-24), w1 = H L - A
-// (A in bits 7-0).  "Byte index" below numbers the 8 bytes of {w1:w0} as the
-// permute does: 0 E, 1 D, 2 C, 3 B, 4 A, 5 unused, 6 L, 7 H; 12 reads zero.
+// Nearly every word is an operand of one datapath instruction as it stands:
+// a byte-permute selector, a bit-field offset, an AND/XOR mask or a pair of
+// 16-bit address deltas.  Values that depend on the instruction's immediate
+// bytes (imm16, 0xFF00 | a8, sign-extended e8, the JR displacement) are
+// bound into the record when it is built (bind_bytes), so the datapath does
+// no per-opcode selection at all.
+//
+// Byte permutes (V_PERM_B32): result byte k is byte sel_k of the 8-byte value
+// {S0:S1} (S1 = bytes 0-3); selectors 8..11 replicate the sign bit of byte
+// 1, 3, 5, 7; 12 reads 0x00; 13 reads 0xFF.  The operand spaces:
+//   registers  {W1:W0}   W0 = B C D E, W1 = H L F A  (0 E, 1 D, 2 C, 3 B, 4 A, 5 F, 6 L, 7 H)
+//   bus        {X1:X0}   X0 = rd0 rd1 Klo Khi, X1 = PC, SP  (0 rd0, 1 rd1, 2/3 K, 4/5 PC, 6/7 SP)
+//   writeback  {U:W}     U = result, new F, v16 lo, v16 hi  (0-3 keep W byte, 4 res, 5 F, 6/7 v16)
+//   write data {U:SEQ}   SEQ = pc + length  (0/1 SEQ lo/hi, 4-7 U)
+//   shifter    {CW:XW}   XW = x x 0 0, CW = W1 << 19 (C flag in bit 31)
+//   flag src   {T16:XW}  T16 = carry vector of the 16-bit adder
 //
 // w0  [0:7] opcode  [8:15] byte 1  [16:23] byte 2  [24:25] length
 //     [26:28] cycles/4 (branch taken or unconditional)  [29:31] cycles/4 not taken
-// w1  8-bit datapath
-//     [0:3]   xi     byte index of the first ALU operand
-//     [4]     xmem   first operand is the bus byte rd0
-//     [5:8]   yi     byte index of the second operand (ysrc 0)
-//     [9:11]  ysrc   second operand: 0 register yi, 1 rd0, 2 const8, 3 byte 1, 4 rd1
-//     [12:13] unit   0 none, 1 adder, 2 logic, 3 shifter
-//     [14]    sub    adder subtracts (second operand complemented, carry inverted)
-//     [15]    usec   adder adds the carry flag (ADC, SBC)
-//     [16]    mA     logic result includes x AND y
-//     [17]    mX     logic result includes x XOR y (both: OR; neither: 0)
-//     [18:21] ib     shifter in-bit: bit ib of (C flag << 9 | x): 7, 0, 9 or 10 (zero)
-//     [22:24] shamt  shifter right shift of the 16-bit funnel: 7 left, 1 right, 4 swap
-//     [25:28] cbit   shifter carry-out: bit cbit of x (8 = zero, for SWAP)
-//     [29]    hi_in  funnel high byte is the in-bit (right shifts), else x
-//     [30]    lo_in  funnel low byte is in-bit << 7 (left shifts), else x
-//     [31]    daa    decimal adjust
-// w2  [0:7]   const8 constant second operand (1, bit masks, 0xFF) or a 16-bit
-//                    addend sign-extended (INC/DEC rr: 1, -1; LD SP,HL: 0)
-//     [8:10]  am     bus address mode of the read/write operand (Am)
-//     [12:15] K      flags kept from F (Z N H C = bits 15..12)
-//     [16:17] nr     bus reads (0, 1, or 2 for POP/RET)
-//     [18:19] hlinc  HL post-update: 0 none, 1 HL+1, 2 HL-1
-//     [20:23] S      flags set to 1
-//     [24:27] X      flags inverted after the keep mask (CCF)
-//     [28:31] E      flags taken from the computed Z/H/C of the active unit
-// w3  register writeback byte masks at bits 2, 10, 18, 26 (w0 bytes 0..3) and
-//     3, 11, 19, 27 (w1 bytes 0..3), interleaved with:
-//     [0]     wmem   the 8-bit result is written to the bus at the operand address
-//     [1]     hlw    w1 takes (HL value << 16 | result), else the result in every byte
-//     [4:7]   op16   stack / control micro-op (Op16)
-//     [8:9]   a16    16-bit adder first operand: 0 zero, 1 source pair, 2 HL, 3 SP
-//     [12:14] b16    second operand: 0 imm16, 1 sext(const8), 2 source pair, 3 sext(byte 1), 4 rd1:rd0
-//     [15]    spw    SP takes the 16-bit result
-//     [16]    w0p    w0 takes the 16-bit result in both halves, else the 8-bit result
-//     [17]    f16    H/C come from the 16-bit adder (ADD HL,rr; SP+e8)
-//     [20:21] rr     source pair: 0 BC, 1 DE, 2 HL, 3 SP (AF with af)
-//     [22]    af     source pair is AF (PUSH AF)
-//     [23]    spadd  16-bit flags use the SP+e8 rule (low nibble / low byte)
-//     [24]    popaf  F takes rd0 & 0xF0 (POP AF)
-//     [28:30] cc     branch condition: 0 always, 1 NZ, 2 Z, 3 NC, 4 C
+// w1  RAP   bus address from the registers        (operand address = RAP | RAQ result)
+// w2  RAQ   bus address from {X1:K}
+// w3  XYP   ALU operands x (byte 0) and y (byte 1) from the registers
+// w4  XYQ   ALU operands from the bus space
+// w5  ABP   16-bit adder operands A (bytes 0-1) and B (bytes 2-3) from the registers
+// w6  ABQ   16-bit adder operands from the bus space
+// w7  KW    [0:7] F source for kept flags (1 F, 4 rd0)  [8:9] bus reads  [12:14] immediate
+//           binding (KMode)  [16:31] K, the record's 16-bit constant
+// w8  SW0   writeback selector of W0
+// w9  SW1   writeback selector of W1 (F always takes the new flags)
+// w10 FL    [0:7] flags taken from the computed Z/H/C  [8:15] flags not forced to 0
+//           [16:23] flags inverted last  [24] IME write  [25] IME value  [26] HALT
+//           [27] trap  [28] SP takes the 16-bit sum  [29] DAA
+// w11 TN    not taken [0:4] cycles [5:6] bus writes [7:9] SP delta (signed);
+//           taken the same at [16:25]
+// w12 TW    [0:4] branch test bit of W1 ^ TW  [8:15] its inversion mask
+//           [16:31] write-data selector (bytes 0-1: first and second written byte)
+// w13 CIW   [0:4] carry-in bit of W1 ^ CIW  [5] logic OR term  [6] logic AND term
+//           [8:15] subtract mask (0xFF: y complemented)  [16:31] flag-source selector
+// w14 SHW   [0:15] shifter funnel selector  [16:20] funnel right shift  [24:31] adder
+//           result mask (0xFF)
+// w15 DW    bus write addresses: operand address + DW, per 16-bit half (wrapping)
 #pragma once
 #include <stdint.h>
 
 namespace gbx {
 
-enum Op16 : uint32_t {
-  O_NONE = 0, O_PUSH, O_POP, O_STSP, O_JR, O_JP, O_JPHL, O_CALL, O_RET, O_RETI, O_RST,
-  O_DI, O_EI, O_HALT, O_TRAP
-};
-enum Am : uint32_t { AM_NONE = 0, AM_HL, AM_BC, AM_DE, AM_A16, AM_A8, AM_C, AM_SP };
-enum Unit : uint32_t { U_NONE = 0, U_ADD, U_LOGIC, U_SHIFT };
-enum YSrc : uint32_t { Y_REG = 0, Y_RD0, Y_CONST, Y_IMM, Y_RD1 };
-// flag bits inside a nibble: Z N H C
-constexpr uint32_t FZ = 8, FN = 4, FH = 2, FC = 1, FALL = 15;
-constexpr uint32_t kZeroByte = 12;  // permute selector that reads 0
-
+constexpr int kRecWords = 16;
 struct Rec {
-  uint32_t w0, w1, w2, w3;
+  uint32_t w[kRecWords];
 };
 
-// byte index of 8-bit register r in B C D E H L (HL) A order
-__host__ __device__ constexpr uint32_t reg_byte(uint32_t r) {
-  return r == 0 ? 3 : r == 1 ? 2 : r == 2 ? 1 : r == 3 ? 0 : r == 4 ? 7 : r == 5 ? 6 : 4;
+// selector values
+enum : uint32_t { P_E = 0, P_D = 1, P_C = 2, P_B = 3, P_A = 4, P_F = 5, P_L = 6, P_H = 7 };
+enum : uint32_t { Q_RD0 = 0, Q_RD1 = 1, Q_KL = 2, Q_KH = 3, Q_PCL = 4, Q_PCH = 5, Q_SPL = 6, Q_SPH = 7 };
+enum : uint32_t { U_RES = 4, U_FN = 5, U_VL = 6, U_VH = 7 };
+enum : uint32_t { S_SEQL = 0, S_SEQH = 1 };
+enum : uint32_t { SH_X = 0, SH_X7 = 8, SH_CF = 11 };
+enum : uint32_t { FS_X = 0, FS_X7 = 8, FS_T0 = 4, FS_T1 = 5, FS_T2 = 6 };
+constexpr uint32_t SEL0 = 12, SELFF = 13;
+constexpr uint32_t kZero4 = 0x0C0C0C0Cu;
+
+// flag bits of F
+constexpr uint32_t FZ = 0x80, FN = 0x40, FH = 0x20, FC = 0x10, FALL = 0xF0;
+
+// How K is bound from the instruction bytes.
+enum KMode : uint32_t { KM_CONST = 0, KM_IMM8, KM_IMM16, KM_HIGH, KM_SEXT, KM_REL };
+// Branch condition (bit of W1 ^ TW that decides "taken").
+enum Cond : uint32_t { C_NEVER = 0, C_ALWAYS, C_NZ, C_Z, C_NC, C_C };
+// Register pairs
+enum Pair : uint32_t { PR_BC = 0, PR_DE, PR_HL, PR_SP, PR_AF, PR_PC, PR_K, PR_RD, PR_ZERO };
+
+__host__ __device__ constexpr uint32_t sel4(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
 }
-// writeback mask bits in w3 for the byte index of a register
-__host__ __device__ constexpr uint32_t wb_bit(uint32_t byte) {
-  return byte < 4 ? 1u << (2 + 8 * byte) : 1u << (3 + 8 * (byte - 4));
-}
-__host__ __device__ constexpr uint32_t wb_pair(uint32_t rr) {  // BC DE HL
-  return rr == 0 ? wb_bit(2) | wb_bit(3) : rr == 1 ? wb_bit(0) | wb_bit(1) : wb_bit(6) | wb_bit(7);
+__host__ __device__ constexpr uint32_t set_byte(uint32_t w, uint32_t k, uint32_t v) {
+  return (w & ~(0xFFu << (8 * k))) | (v << (8 * k));
 }
 
 struct Dec {
-  uint32_t len = 1, cyc4 = 1, cycnt4 = 0;
-  uint32_t xi = kZeroByte, xmem = 0, yi = kZeroByte, ysrc = Y_REG, unit = U_NONE, sub = 0, usec = 0,
-           mA = 0, mX = 0, ib = 10, shamt = 0, cbit = 8, hi_in = 0, lo_in = 0, daa = 0;
-  uint32_t const8 = 0, am = AM_NONE, K = FALL, nr = 0, hlinc = 0, S = 0, X = 0, E = 0;
-  uint32_t wb = 0, wmem = 0, hlw = 0, op16 = O_NONE, a16 = 0, b16 = 0, spw = 0, w0p = 0, f16 = 0,
-           rr = 0, af = 0, spadd = 0, popaf = 0, cc = 0;
+  uint32_t len = 1, cyc = 4, cycnt = 0xFF;  // T-cycles; cycnt 0xFF: same as cyc
+  uint32_t rap = kZero4, raq = kZero4, nr = 0;
+  uint32_t xyp = kZero4, xyq = kZero4, abp = kZero4, abq = kZero4;
+  uint32_t fsrc = 1, kmode = KM_CONST, k = 0;
+  uint32_t sw0 = 0x03020100u, sw1 = 0x03020000u | (U_FN << 8);
+  uint32_t E = 0, M = FALL, X = 0;
+  uint32_t ime_set = 0, ime_on = 0, halt = 0, trap = 0, spw = 0, daa = 0;
+  uint32_t cond = C_NEVER;
+  uint32_t wn = 0, dsp = 0, wn_nt = 0xFF, dsp_nt = 0xFF;  // taken/unconditional; not taken
+  uint32_t wv = (SEL0 << 8) | U_RES;
+  uint32_t cipos = 9, lor = 0, land = 0, subm = 0, fsel = 0x0C0Cu;
+  uint32_t shsel = 0x0C0Cu, sh = 0, madd = 0;
+  uint32_t dw = 0;
 };
 
-__host__ __device__ constexpr Rec pack(Dec d) {
-  if (d.cycnt4 == 0) d.cycnt4 = d.cyc4;
-  Rec r{};
-  r.w0 = (d.len << 24) | (d.cyc4 << 26) | (d.cycnt4 << 29);
-  r.w1 = d.xi | (d.xmem << 4) | (d.yi << 5) | (d.ysrc << 9) | (d.unit << 12) | (d.sub << 14) |
-         (d.usec << 15) | (d.mA << 16) | (d.mX << 17) | (d.ib << 18) | (d.shamt << 22) |
-         (d.cbit << 25) | (d.hi_in << 29) | (d.lo_in << 30) | (d.daa << 31);
-  r.w2 = (d.const8 & 0xFFu) | (d.am << 8) | (d.K << 12) | (d.nr << 16) | (d.hlinc << 18) |
-         (d.S << 20) | (d.X << 24) | (d.E << 28);
-  r.w3 = d.wb | d.wmem | (d.hlw << 1) | (d.op16 << 4) | (d.a16 << 8) | (d.b16 << 12) |
-         (d.spw << 15) | (d.w0p << 16) | (d.f16 << 17) | (d.rr << 20) | (d.af << 22) |
-         (d.spadd << 23) | (d.popaf << 24) | (d.cc << 28);
-  return r;
+// 8-bit register r in opcode order B C D E H L (HL) A: permute byte, and
+// the writeback word (0 W0, 1 W1) and byte it lives in.
+__host__ __device__ constexpr uint32_t reg_sel(uint32_t r) {
+  return r == 0 ? P_B : r == 1 ? P_C : r == 2 ? P_D : r == 3 ? P_E : r == 4 ? P_H : r == 5 ? P_L : P_A;
 }
 
-// 8-bit destination: register r (writeback mask) or the bus operand (r = 6)
+__host__ __device__ constexpr void wb8(Dec& d, uint32_t r, uint32_t src) {
+  const uint32_t s = reg_sel(r);
+  if (s < 4) d.sw0 = set_byte(d.sw0, s, src);
+  else if (s == P_A) d.sw1 = set_byte(d.sw1, 0, src);
+  else d.sw1 = set_byte(d.sw1, s - 4, src);  // L byte 2, H byte 3
+}
+// 16-bit writeback of v16 to a pair (BC DE HL SP)
+__host__ __device__ constexpr void wb16(Dec& d, uint32_t p) {
+  if (p == PR_BC) d.sw0 = (d.sw0 & 0x0000FFFFu) | (U_VL << 16) | (U_VH << 24);
+  else if (p == PR_DE) d.sw0 = (d.sw0 & 0xFFFF0000u) | U_VL | (U_VH << 8);
+  else if (p == PR_HL) d.sw1 = (d.sw1 & 0x0000FFFFu) | (U_VL << 16) | (U_VH << 24);
+  else d.spw = 1;
+}
+// a 16-bit source placed at byte pair `at` (0: A operand / address, 2: B operand)
+// of the register-space and bus-space selectors
+__host__ __device__ constexpr void src16(uint32_t& p, uint32_t& q, uint32_t at, uint32_t pr) {
+  uint32_t lo = SEL0, hi = SEL0, qlo = SEL0, qhi = SEL0;
+  if (pr == PR_BC) { lo = P_C; hi = P_B; }
+  else if (pr == PR_DE) { lo = P_E; hi = P_D; }
+  else if (pr == PR_HL) { lo = P_L; hi = P_H; }
+  else if (pr == PR_AF) { lo = P_F; hi = P_A; }
+  else if (pr == PR_SP) { qlo = Q_SPL; qhi = Q_SPH; }
+  else if (pr == PR_PC) { qlo = Q_PCL; qhi = Q_PCH; }
+  else if (pr == PR_K) { qlo = Q_KL; qhi = Q_KH; }
+  else if (pr == PR_RD) { qlo = Q_RD0; qhi = Q_RD1; }
+  p = set_byte(set_byte(p, at, lo), at + 1, hi);
+  q = set_byte(set_byte(q, at, qlo), at + 1, qhi);
+}
+__host__ __device__ constexpr void set_a16(Dec& d, uint32_t pr) { src16(d.abp, d.abq, 0, pr); }
+__host__ __device__ constexpr void set_b16(Dec& d, uint32_t pr) { src16(d.abp, d.abq, 2, pr); }
+__host__ __device__ constexpr void set_addr(Dec& d, uint32_t pr) { src16(d.rap, d.raq, 0, pr); }
+
+// ALU operand x (byte 0) or y (byte 1) from register r (6: the bus byte rd0,
+// 8: K low byte, 9: rd1)
+__host__ __device__ constexpr void set_xy(Dec& d, uint32_t at, uint32_t r) {
+  if (r == 6) d.xyq = set_byte(d.xyq, at, Q_RD0);
+  else if (r == 8) d.xyq = set_byte(d.xyq, at, Q_KL);
+  else if (r == 9) d.xyq = set_byte(d.xyq, at, Q_RD1);
+  else d.xyp = set_byte(d.xyp, at, reg_sel(r));
+}
+__host__ __device__ constexpr void set_x(Dec& d, uint32_t r) { set_xy(d, 0, r); }
+__host__ __device__ constexpr void set_y(Dec& d, uint32_t r) { set_xy(d, 1, r); }
+
+// 8-bit destination: register r, or the bus operand (r = 6)
 __host__ __device__ constexpr void set_dst(Dec& d, uint32_t r) {
-  if (r == 6) d.wmem = 1;
-  else d.wb = wb_bit(reg_byte(r));
+  if (r == 6) d.wn = 1;
+  else wb8(d, r, U_RES);
 }
-// second operand from register r, the bus (r = 6) or the immediate byte (r = 8)
-__host__ __device__ constexpr void set_y(Dec& d, uint32_t r) {
-  if (r == 6) d.ysrc = Y_RD0;
-  else if (r == 8) d.ysrc = Y_IMM;
-  else d.yi = reg_byte(r);
-}
-// first operand from register r or the bus (r = 6)
-__host__ __device__ constexpr void set_x(Dec& d, uint32_t r) {
-  if (r == 6) d.xmem = 1;
-  else d.xi = reg_byte(r);
+// register move / load / store: res = 0 + y
+__host__ __device__ constexpr void set_mov(Dec& d) { d.madd = 0xFF; }
+
+// 8-bit ALU op of opcode bits 5-3: ADD ADC SUB SBC AND XOR OR CP (alu.py)
+__host__ __device__ constexpr void set_alu(Dec& d, uint32_t y) {
+  set_x(d, 7);
+  if (y <= 3 || y == 7) {
+    const bool sub = y == 2 || y == 3 || y == 7;
+    d.madd = 0xFF;
+    d.subm = sub ? 0xFF : 0;
+    d.cipos = (y == 1 || y == 3) ? 12 : 9;
+    d.E = FZ | FH | FC;
+    d.M = FZ | FH | FC;  // N forced: set (subtraction) or clear
+    d.X = sub ? FN | FH | FC : 0;  // subtraction: borrows are the inverted carries
+  } else {
+    d.land = (y == 4 || y == 5) ? 1 : 0;
+    d.lor = (y == 5 || y == 6) ? 1 : 0;
+    d.E = FZ;
+    d.M = FZ;
+    d.X = y == 4 ? FH : 0;
+  }
+  if (y != 7) wb8(d, 7, U_RES);
 }
 
-// 8-bit ALU op of opcode bits 5-3 in 0x80-0xBF / 0xC6-0xFE: ADD ADC SUB SBC AND XOR OR CP
-__host__ __device__ constexpr void set_alu(Dec& d, uint32_t y) {
-  d.xi = reg_byte(7);
-  d.K = 0;
-  if (y <= 3 || y == 7) {
-    d.unit = U_ADD;
-    d.sub = (y == 2 || y == 3 || y == 7) ? 1 : 0;
-    d.usec = (y == 1 || y == 3) ? 1 : 0;
-    d.S = d.sub ? FN : 0;
-    d.E = FZ | FH | FC;
-  } else {
-    d.unit = U_LOGIC;
-    d.mA = (y == 4 || y == 6) ? 1 : 0;
-    d.mX = (y == 5 || y == 6) ? 1 : 0;
-    d.S = y == 4 ? FH : 0;
-    d.E = FZ;
-  }
-  if (y != 7) d.wb = wb_bit(reg_byte(7));
-}
-// shifter op sub (CB order RLC RRC RL RR SLA SRA SWAP SRL)
+// shifter op sub (CB order RLC RRC RL RR SLA SRA SWAP SRL; bitops.py): a
+// 16-bit funnel (hi << 8 | lo) shifted right by 7 (left ops), 1 (right ops)
+// or 4 (SWAP); the carry out is bit 7 or bit 0 of x.
 __host__ __device__ constexpr void set_shift(Dec& d, uint32_t sub) {
-  d.unit = U_SHIFT;
   const bool left = sub == 0 || sub == 2 || sub == 4;
-  if (sub == 6) {
-    d.shamt = 4;
-    d.cbit = 8;
-  } else if (left) {
-    d.shamt = 7;
-    d.lo_in = 1;
-    d.cbit = 7;
-    d.ib = sub == 0 ? 7 : sub == 2 ? 9 : 10;
-  } else {
-    d.shamt = 1;
-    d.hi_in = 1;
-    d.cbit = 0;
-    d.ib = sub == 1 ? 0 : sub == 3 ? 9 : sub == 5 ? 7 : 10;
-  }
-  d.K = 0;
+  uint32_t lo = SH_X, hi = SH_X, c = FS_X;
+  if (sub == 2) lo = SH_CF;
+  if (sub == 4) lo = SEL0;
+  if (sub == 3) hi = SH_CF;
+  if (sub == 5) hi = SH_X7;
+  if (sub == 7) hi = SEL0;
+  if (left) c = FS_X7;
+  if (sub == 6) c = SEL0;
+  d.shsel = lo | (hi << 8);
+  d.sh = sub == 6 ? 4 : left ? 7 : 1;
+  d.fsel = SEL0 | (c << 8);
   d.E = FZ | FC;
+  d.M = FZ | FC;
 }
 
 // CB-prefixed instruction (second byte cb).  bitops.py: rotates/shifts,
 // BIT (flags only), RES, SET; (HL) forms read and write back the bus.
-__host__ __device__ constexpr Rec decode_cb(uint32_t cb) {
+__host__ __device__ constexpr Dec decode_cb(uint32_t cb) {
   Dec d;
   const uint32_t idx = cb & 7u, grp = cb >> 6, sub = (cb >> 3) & 7u;
   d.len = 2;
   set_x(d, idx);
   if (idx == 6) {
-    d.am = AM_HL;
+    set_addr(d, PR_HL);
     d.nr = 1;
-    d.cyc4 = grp == 1 ? 3 : 4;
+    d.cyc = grp == 1 ? 12 : 16;
   } else {
-    d.cyc4 = 2;
+    d.cyc = 8;
   }
   if (grp == 0) {
     set_shift(d, sub);
     set_dst(d, idx);
   } else {
-    d.unit = U_LOGIC;
-    d.ysrc = Y_CONST;
-    d.mA = 1;
+    set_y(d, 8);
     if (grp == 1) {  // BIT: Z = bit clear, H = 1, C kept
-      d.const8 = 1u << sub;
-      d.K = FC;
-      d.S = FH;
+      d.land = 1;
+      d.k = 1u << sub;
       d.E = FZ;
+      d.M = FZ | FC;
+      d.X = FH;
     } else {
       if (grp == 2) {  // RES: x AND ~bit
-        d.const8 = ~(1u << sub) & 0xFFu;
+        d.land = 1;
+        d.k = ~(1u << sub) & 0xFFu;
       } else {  // SET: x OR bit
-        d.mX = 1;
-        d.const8 = 1u << sub;
+        d.lor = 1;
+        d.k = 1u << sub;
       }
       set_dst(d, idx);
     }
   }
-  return pack(d);
+  return d;
 }
 
-__host__ __device__ constexpr Rec decode_op(uint32_t op) {
+__host__ __device__ constexpr Dec decode_op(uint32_t op) {
   Dec d;
   const uint32_t y = (op >> 3) & 7u, z = op & 7u, p = (op >> 4) & 3u;
   if (op == 0x76u) {  // HALT
-    d.op16 = O_HALT;
-    return pack(d);
+    d.halt = 1;
+    return d;
   }
   if (op >= 0x40u && op < 0x80u) {  // LD r,r' / LD r,(HL) / LD (HL),r
-    d.unit = U_LOGIC;
-    d.mX = 1;  // 0 ^ y
+    set_mov(d);
     set_y(d, z);
     set_dst(d, y);
     if (y == 6 || z == 6) {
-      d.am = AM_HL;
-      d.cyc4 = 2;
+      set_addr(d, PR_HL);
+      d.cyc = 8;
       d.nr = z == 6 ? 1 : 0;
     }
-    return pack(d);
+    return d;
   }
   if (op >= 0x80u && op < 0xC0u) {  // ALU A,r / ALU A,(HL)
     set_alu(d, y);
     set_y(d, z);
     if (z == 6) {
-      d.am = AM_HL;
+      set_addr(d, PR_HL);
       d.nr = 1;
-      d.cyc4 = 2;
+      d.cyc = 8;
     }
-    return pack(d);
+    return d;
   }
+  const uint32_t pair = p == 3 ? PR_SP : p;  // BC DE HL SP
   switch (op) {
-    case 0x00: return pack(d);  // NOP
-    case 0xF3: d.op16 = O_DI; return pack(d);
-    case 0xFB: d.op16 = O_EI; return pack(d);
+    case 0x00: return d;  // NOP
+    case 0xF3: d.ime_set = 1; return d;                 // DI
+    case 0xFB: d.ime_set = 1; d.ime_on = 1; return d;   // EI (immediate)
     case 0x01: case 0x11: case 0x21: case 0x31:  // LD rr,d16
-      d.len = 3; d.cyc4 = 3; d.a16 = 0; d.b16 = 0;
-      if (p == 3) d.spw = 1;
-      else if (p == 2) { d.hlw = 1; d.wb = wb_pair(2); }
-      else { d.w0p = 1; d.wb = wb_pair(p); }
-      return pack(d);
+      d.len = 3; d.cyc = 12; d.kmode = KM_IMM16; set_b16(d, PR_K); wb16(d, pair);
+      return d;
     case 0x03: case 0x13: case 0x23: case 0x33:  // INC rr
     case 0x0B: case 0x1B: case 0x2B: case 0x3B:  // DEC rr
-      d.cyc4 = 2; d.rr = p; d.a16 = 1; d.b16 = 1; d.const8 = (op & 8u) ? 0xFFu : 1u;
-      if (p == 3) d.spw = 1;
-      else if (p == 2) { d.hlw = 1; d.wb = wb_pair(2); }
-      else { d.w0p = 1; d.wb = wb_pair(p); }
-      return pack(d);
-    case 0x09: case 0x19: case 0x29: case 0x39:  // ADD HL,rr (alu.py:72-111)
-      d.cyc4 = 2; d.rr = p; d.a16 = 2; d.b16 = 2; d.hlw = 1; d.wb = wb_pair(2);
-      d.f16 = 1; d.K = FZ; d.E = FH | FC;
-      return pack(d);
+      d.cyc = 8; set_a16(d, pair); set_b16(d, PR_K); d.k = (op & 8u) ? 0xFFFFu : 1u;
+      wb16(d, pair);
+      return d;
+    case 0x09: case 0x19: case 0x29: case 0x39:  // ADD HL,rr (alu.py:72-111): H bit 11, C bit 15
+      d.cyc = 8; set_a16(d, PR_HL); set_b16(d, pair); wb16(d, PR_HL);
+      d.fsel = FS_T1 | (FS_T2 << 8); d.E = FH | FC; d.M = FZ | FH | FC;
+      return d;
     case 0xF9:  // LD SP,HL
-      d.cyc4 = 2; d.a16 = 2; d.b16 = 1; d.const8 = 0; d.spw = 1;
-      return pack(d);
+      d.cyc = 8; set_a16(d, PR_HL); d.spw = 1;
+      return d;
     case 0x02: case 0x12: case 0x22: case 0x32:  // LD (BC)/(DE)/(HL+)/(HL-),A
-      d.cyc4 = 2; d.unit = U_LOGIC; d.mX = 1; set_y(d, 7); d.wmem = 1;
-      d.am = op == 0x02 ? AM_BC : op == 0x12 ? AM_DE : AM_HL;
+      d.cyc = 8; set_mov(d); set_y(d, 7); d.wn = 1;
+      set_addr(d, op == 0x02 ? PR_BC : op == 0x12 ? PR_DE : PR_HL);
       if (op == 0x22 || op == 0x32) {
-        d.hlinc = op == 0x22 ? 1 : 2; d.hlw = 1; d.wb = wb_pair(2);
+        set_a16(d, PR_HL); set_b16(d, PR_K); d.k = op == 0x22 ? 1u : 0xFFFFu; wb16(d, PR_HL);
       }
-      return pack(d);
+      return d;
     case 0x0A: case 0x1A: case 0x2A: case 0x3A:  // LD A,(BC)/(DE)/(HL+)/(HL-)
-      d.cyc4 = 2; d.unit = U_LOGIC; d.mX = 1; d.ysrc = Y_RD0; d.nr = 1;
-      d.wb = wb_bit(reg_byte(7));
-      d.am = op == 0x0A ? AM_BC : op == 0x1A ? AM_DE : AM_HL;
+      d.cyc = 8; set_mov(d); set_y(d, 6); d.nr = 1; wb8(d, 7, U_RES);
+      set_addr(d, op == 0x0A ? PR_BC : op == 0x1A ? PR_DE : PR_HL);
       if (op == 0x2A || op == 0x3A) {
-        d.hlinc = op == 0x2A ? 1 : 2; d.hlw = 1; d.wb |= wb_pair(2);
+        set_a16(d, PR_HL); set_b16(d, PR_K); d.k = op == 0x2A ? 1u : 0xFFFFu; wb16(d, PR_HL);
       }
-      return pack(d);
+      return d;
     case 0xEA: case 0xE0: case 0xE2:  // LD (a16),A / LDH (a8),A / LD (C),A
-      d.len = op == 0xEA ? 3 : op == 0xE0 ? 2 : 1;
-      d.cyc4 = op == 0xEA ? 4 : op == 0xE0 ? 3 : 2;
-      d.am = op == 0xEA ? AM_A16 : op == 0xE0 ? AM_A8 : AM_C;
-      d.unit = U_LOGIC; d.mX = 1; set_y(d, 7); d.wmem = 1;
-      return pack(d);
     case 0xFA: case 0xF0: case 0xF2:  // LD A,(a16) / LDH A,(a8) / LD A,(C)
-      d.len = op == 0xFA ? 3 : op == 0xF0 ? 2 : 1;
-      d.cyc4 = op == 0xFA ? 4 : op == 0xF0 ? 3 : 2;
-      d.am = op == 0xFA ? AM_A16 : op == 0xF0 ? AM_A8 : AM_C;
-      d.unit = U_LOGIC; d.mX = 1; d.ysrc = Y_RD0; d.nr = 1; d.wb = wb_bit(reg_byte(7));
-      return pack(d);
+      d.len = (op & 0xFu) == 0xAu ? 3 : (op & 0xFu) == 0x0u ? 2 : 1;
+      d.cyc = (op & 0xFu) == 0xAu ? 16 : (op & 0xFu) == 0x0u ? 12 : 8;
+      if ((op & 0xFu) == 0x2u) d.rap = sel4(P_C, SELFF, SEL0, SEL0);  // 0xFF00 | C
+      else { set_addr(d, PR_K); d.kmode = (op & 0xFu) == 0xAu ? KM_IMM16 : KM_HIGH; }
+      set_mov(d);
+      if (op < 0xF0u) { set_y(d, 7); d.wn = 1; }
+      else { set_y(d, 6); d.nr = 1; wb8(d, 7, U_RES); }
+      return d;
     case 0x36:  // LD (HL),d8
-      d.len = 2; d.cyc4 = 3; d.am = AM_HL; d.unit = U_LOGIC; d.mX = 1; d.ysrc = Y_IMM; d.wmem = 1;
-      return pack(d);
+      d.len = 2; d.cyc = 12; set_addr(d, PR_HL); set_mov(d); set_y(d, 8); d.kmode = KM_IMM8;
+      d.wn = 1;
+      return d;
     case 0x06: case 0x0E: case 0x16: case 0x1E: case 0x26: case 0x2E: case 0x3E:  // LD r,d8
-      d.len = 2; d.cyc4 = 2; d.unit = U_LOGIC; d.mX = 1; d.ysrc = Y_IMM; set_dst(d, y);
-      return pack(d);
+      d.len = 2; d.cyc = 8; set_mov(d); set_y(d, 8); d.kmode = KM_IMM8; set_dst(d, y);
+      return d;
     case 0x04: case 0x0C: case 0x14: case 0x1C: case 0x24: case 0x2C: case 0x3C:
     case 0x05: case 0x0D: case 0x15: case 0x1D: case 0x25: case 0x2D: case 0x3D:
-    case 0x34: case 0x35:  // INC/DEC r, (HL): alu.py:13-22, 208-217, 913-946
-      d.unit = U_ADD; d.sub = op & 1u; d.ysrc = Y_CONST; d.const8 = 1;
+    case 0x34: case 0x35: {  // INC/DEC r, (HL): alu.py:13-22, 208-217, 913-946
+      const bool dec = (op & 1u) != 0u;
+      d.madd = 0xFF; d.subm = dec ? 0xFF : 0; set_y(d, 8); d.k = 1;
       set_x(d, y); set_dst(d, y);
-      d.K = FC; d.S = d.sub ? FN : 0; d.E = FZ | FH;
-      if (y == 6) { d.am = AM_HL; d.nr = 1; d.cyc4 = 3; }
-      return pack(d);
+      d.E = FZ | FH; d.M = FZ | FH | FC; d.X = dec ? FN | FH : 0;
+      if (y == 6) { set_addr(d, PR_HL); d.nr = 1; d.cyc = 12; }
+      return d;
+    }
     case 0x07: case 0x0F: case 0x17: case 0x1F:  // RLCA RRCA RLA RRA (Z cleared)
-      set_shift(d, y); set_x(d, 7); set_dst(d, 7); d.E = FC;
-      return pack(d);
+      set_shift(d, y); set_x(d, 7); set_dst(d, 7); d.E = FC; d.M = FC;
+      return d;
     case 0x27:  // DAA (alu.py:897-950): N kept, H cleared, Z and C computed
-      set_x(d, 7); set_dst(d, 7); d.daa = 1; d.K = FN; d.E = FZ | FC;
-      return pack(d);
-    case 0x2F:  // CPL
-      set_x(d, 7); set_dst(d, 7); d.unit = U_LOGIC; d.mX = 1; d.ysrc = Y_CONST; d.const8 = 0xFF;
-      d.K = FZ | FC; d.S = FN | FH;
-      return pack(d);
-    case 0x37: d.K = FZ; d.S = FC; return pack(d);               // SCF
-    case 0x3F: d.K = FZ | FC; d.X = FC; return pack(d);          // CCF
+      set_x(d, 7); set_mov(d); set_dst(d, 7); d.daa = 1; d.E = FZ | FC; d.M = FZ | FN | FC;
+      return d;
+    case 0x2F:  // CPL: x XOR 0xFF, N and H set
+      set_x(d, 7); set_y(d, 8); d.k = 0xFF; d.lor = 1; d.land = 1; set_dst(d, 7);
+      d.M = FZ | FC; d.X = FN | FH;
+      return d;
+    case 0x37: d.M = FZ; d.X = FC; return d;          // SCF
+    case 0x3F: d.M = FZ | FC; d.X = FC; return d;     // CCF
     case 0xC6: case 0xCE: case 0xD6: case 0xDE: case 0xE6: case 0xEE: case 0xF6: case 0xFE:
-      d.len = 2; d.cyc4 = 2; set_alu(d, y); d.ysrc = Y_IMM;
-      return pack(d);
-    // control flow
-    case 0x18: d.len = 2; d.cyc4 = 3; d.op16 = O_JR; return pack(d);
-    case 0x20: case 0x28: case 0x30: case 0x38:
-      d.len = 2; d.cyc4 = 3; d.cycnt4 = 2; d.op16 = O_JR; d.cc = (y & 3u) + 1u;
-      return pack(d);
-    case 0xC3: d.len = 3; d.cyc4 = 4; d.op16 = O_JP; return pack(d);
-    case 0xC2: case 0xCA: case 0xD2: case 0xDA:
-      d.len = 3; d.cyc4 = 4; d.cycnt4 = 3; d.op16 = O_JP; d.cc = (y & 3u) + 1u;
-      return pack(d);
-    case 0xE9: d.op16 = O_JPHL; return pack(d);
-    case 0xCD: d.len = 3; d.cyc4 = 6; d.op16 = O_CALL; return pack(d);
-    case 0xC4: case 0xCC: case 0xD4: case 0xDC:
-      d.len = 3; d.cyc4 = 6; d.cycnt4 = 3; d.op16 = O_CALL; d.cc = (y & 3u) + 1u;
-      return pack(d);
-    case 0xC9: case 0xD9:
-      d.cyc4 = 4; d.op16 = op == 0xC9 ? O_RET : O_RETI; d.am = AM_SP; d.nr = 2;
-      return pack(d);
-    case 0xC0: case 0xC8: case 0xD0: case 0xD8:
-      d.cyc4 = 5; d.cycnt4 = 2; d.op16 = O_RET; d.am = AM_SP; d.nr = 2; d.cc = (y & 3u) + 1u;
-      return pack(d);
+      d.len = 2; d.cyc = 8; set_alu(d, y); set_y(d, 8); d.kmode = KM_IMM8;
+      return d;
+    // control flow (jumps.py): the target is the 16-bit sum
+    case 0x18: case 0x20: case 0x28: case 0x30: case 0x38:  // JR [cc],e8
+      d.len = 2; d.cyc = 12; d.kmode = KM_REL; set_a16(d, PR_PC); set_b16(d, PR_K);
+      if (op == 0x18) d.cond = C_ALWAYS;
+      else { d.cond = C_NZ + (y & 3u); d.cycnt = 8; }
+      return d;
+    case 0xC3: case 0xC2: case 0xCA: case 0xD2: case 0xDA:  // JP [cc],a16
+      d.len = 3; d.cyc = 16; d.kmode = KM_IMM16; set_b16(d, PR_K);
+      if (op == 0xC3) d.cond = C_ALWAYS;
+      else { d.cond = C_NZ + (y & 3u); d.cycnt = 12; }
+      return d;
+    case 0xE9:  // JP HL
+      d.cond = C_ALWAYS; set_a16(d, PR_HL);
+      return d;
+    case 0xCD: case 0xC4: case 0xCC: case 0xD4: case 0xDC:  // CALL [cc],a16: push pc + 3
+      d.len = 3; d.cyc = 24; d.kmode = KM_IMM16; set_b16(d, PR_K); set_addr(d, PR_SP);
+      d.wn = 2; d.dsp = 0xFFFEu; d.wv = S_SEQH | (S_SEQL << 8); d.dw = 0xFFFEFFFFu;
+      if (op == 0xCD) d.cond = C_ALWAYS;
+      else { d.cond = C_NZ + (y & 3u); d.cycnt = 12; d.wn_nt = 0; d.dsp_nt = 0; }
+      return d;
+    case 0xC9: case 0xD9: case 0xC0: case 0xC8: case 0xD0: case 0xD8:  // RET [cc], RETI
+      d.cyc = 16; set_addr(d, PR_SP); d.nr = 2; set_b16(d, PR_RD); d.dsp = 2;
+      if (op == 0xC9 || op == 0xD9) d.cond = C_ALWAYS;
+      else { d.cond = C_NZ + (y & 3u); d.cyc = 20; d.cycnt = 8; d.dsp_nt = 0; }
+      if (op == 0xD9) { d.ime_set = 1; d.ime_on = 1; }
+      return d;
     case 0xC7: case 0xCF: case 0xD7: case 0xDF: case 0xE7: case 0xEF: case 0xF7: case 0xFF:
-      d.cyc4 = 4; d.op16 = O_RST; return pack(d);
-    case 0xC5: case 0xD5: case 0xE5: case 0xF5:  // PUSH rr
-      d.cyc4 = 4; d.op16 = O_PUSH; d.rr = p; d.af = p == 3 ? 1 : 0;
-      return pack(d);
+      d.cyc = 16; d.cond = C_ALWAYS; set_b16(d, PR_K); d.k = op & 0x38u; set_addr(d, PR_SP);
+      d.wn = 2; d.dsp = 0xFFFEu; d.wv = S_SEQH | (S_SEQL << 8); d.dw = 0xFFFEFFFFu;
+      return d;
+    case 0xC5: case 0xD5: case 0xE5: case 0xF5:  // PUSH rr (stack.py)
+      d.cyc = 16; set_a16(d, p == 3 ? PR_AF : p); set_addr(d, PR_SP);
+      d.wn = 2; d.dsp = 0xFFFEu; d.wv = U_VH | (U_VL << 8); d.dw = 0xFFFEFFFFu;
+      return d;
     case 0xC1: case 0xD1: case 0xE1: case 0xF1:  // POP rr
-      d.cyc4 = 3; d.op16 = O_POP; d.am = AM_SP; d.nr = 2;
+      d.cyc = 12; set_addr(d, PR_SP); d.nr = 2; set_b16(d, PR_RD); d.dsp = 2;
       if (p == 3) {  // POP AF: A = rd1, F = rd0 & 0xF0
-        d.unit = U_LOGIC; d.mX = 1; d.ysrc = Y_RD1; d.wb = wb_bit(reg_byte(7)); d.popaf = 1;
+        wb8(d, 7, U_VH); d.fsrc = 4; d.M = FALL;
       } else {
-        d.a16 = 0; d.b16 = 4;
-        if (p == 2) { d.hlw = 1; d.wb = wb_pair(2); }
-        else { d.w0p = 1; d.wb = wb_pair(p); }
+        wb16(d, p);
       }
-      return pack(d);
-    case 0xE8: case 0xF8:  // ADD SP,e8 / LD HL,SP+e8 (alu.py:114-177)
-      d.len = 2; d.cyc4 = op == 0xE8 ? 4 : 3; d.a16 = 3; d.b16 = 3;
-      if (op == 0xE8) d.spw = 1;
-      else { d.hlw = 1; d.wb = wb_pair(2); }
-      d.f16 = 1; d.spadd = 1; d.K = 0; d.E = FH | FC;
-      return pack(d);
-    case 0x08: d.len = 3; d.cyc4 = 5; d.op16 = O_STSP; return pack(d);
-    case 0xCB: return Rec{};  // resolved with the second byte (decode_cb)
+      return d;
+    case 0xE8: case 0xF8:  // ADD SP,e8 / LD HL,SP+e8 (alu.py:114-177): H/C from the low byte
+      d.len = 2; d.cyc = op == 0xE8 ? 16 : 12; d.kmode = KM_SEXT; set_a16(d, PR_SP);
+      set_b16(d, PR_K); wb16(d, op == 0xE8 ? PR_SP : PR_HL);
+      d.fsel = FS_T0 | (FS_T1 << 8); d.E = FH | FC; d.M = FH | FC;
+      return d;
+    case 0x08:  // LD (a16),SP
+      d.len = 3; d.cyc = 20; d.kmode = KM_IMM16; set_addr(d, PR_K); set_a16(d, PR_SP);
+      d.wn = 2; d.wv = U_VL | (U_VH << 8); d.dw = 0x00010000u;
+      return d;
     default:  // STOP and the 11 unused opcodes: trap, pc frozen (misc.py:42-56)
-      d.cyc4 = 0;
-      d.op16 = O_TRAP;
-      return pack(d);
+      d.cyc = 0; d.trap = 1; d.cond = C_ALWAYS; set_a16(d, PR_PC);
+      return d;
   }
 }
 
-// Decode of the instruction whose first three bytes are op, b1, b2, with
-// the instruction bytes placed in w0.
-__host__ __device__ constexpr Rec decode_insn(uint32_t op, uint32_t b1, uint32_t b2) {
-  Rec r = op == 0xCBu ? decode_cb(b1) : decode_op(op);
-  r.w0 |= op | (b1 << 8) | (b2 << 16);
+// Branch-test word: bit `pos` of W1 ^ TW decides "taken".  W1 bits 8 and 9
+// are F bits 0-1, always 0: bit 8 inverted reads 1 (always), bit 9 reads 0
+// (never); Z is W1 bit 15 and C W1 bit 12.
+__host__ __device__ constexpr uint32_t cond_word(uint32_t c) {
+  return c == C_ALWAYS ? 8u | (1u << 8)
+         : c == C_NZ   ? 15u | (1u << 15)
+         : c == C_Z    ? 15u
+         : c == C_NC   ? 12u | (1u << 12)
+         : c == C_C    ? 12u
+                       : 9u;
+}
+__host__ __device__ constexpr uint32_t tn_half(uint32_t cyc, uint32_t wn, uint32_t dsp) {
+  return cyc | (wn << 5) | (((dsp & 0xFFFFu) == 0xFFFEu ? 6u : dsp) << 7);
+}
+
+__host__ __device__ constexpr Rec pack(Dec d) {
+  if (d.cycnt == 0xFF) d.cycnt = d.cyc;
+  if (d.wn_nt == 0xFF) d.wn_nt = d.wn;
+  if (d.dsp_nt == 0xFF) d.dsp_nt = d.dsp;
+  Rec r{};
+  r.w[0] = (d.len << 24) | ((d.cyc >> 2) << 26) | ((d.cycnt >> 2) << 29) | d.kmode;
+  r.w[1] = d.rap;
+  r.w[2] = d.raq;
+  r.w[3] = d.xyp;
+  r.w[4] = d.xyq;
+  r.w[5] = d.abp;
+  r.w[6] = d.abq;
+  r.w[7] = d.fsrc | (d.nr << 8) | (d.kmode << 12) | ((d.k & 0xFFFFu) << 16);
+  r.w[8] = d.sw0;
+  r.w[9] = d.sw1;
+  r.w[10] = d.E | (d.M << 8) | (d.X << 16) | (d.ime_set << 24) | (d.ime_on << 25) |
+            (d.halt << 26) | (d.trap << 27) | (d.spw << 28) | (d.daa << 29);
+  // a non-jump is never "taken": its fields live in the not-taken half
+  const uint32_t tk = d.cond == C_NEVER ? 0u : tn_half(d.cyc, d.wn, d.dsp);
+  r.w[11] = tn_half(d.cond == C_NEVER ? d.cyc : d.cycnt, d.wn_nt, d.dsp_nt) | (tk << 16);
+  r.w[12] = cond_word(d.cond) | (d.wv << 16);
+  r.w[13] = d.cipos | (d.lor << 5) | (d.land << 6) | (d.subm << 8) | (d.fsel << 16);
+  r.w[14] = d.shsel | (d.sh << 16) | (d.madd << 24);
+  r.w[15] = d.dw;
   return r;
+}
+
+__host__ __device__ constexpr uint32_t sext8(uint32_t v) { return (uint32_t)(int32_t)(int8_t)(v & 0xFFu); }
+
+// Bind the instruction bytes op, b1, b2 into a record decoded from the
+// opcode alone: the bytes go into w0, K into KW per the record's KMode.
+__host__ __device__ constexpr Rec bind_bytes(Rec r, uint32_t op, uint32_t b1, uint32_t b2) {
+  const uint32_t km = r.w[0] & 7u;
+  uint32_t k = r.w[7] >> 16;
+  if (km == KM_IMM8) k = b1;
+  else if (km == KM_IMM16) k = b1 | (b2 << 8);
+  else if (km == KM_HIGH) k = 0xFF00u | b1;
+  else if (km == KM_SEXT) k = sext8(b1) & 0xFFFFu;
+  else if (km == KM_REL) k = (2u + sext8(b1)) & 0xFFFFu;
+  r.w[0] = (r.w[0] & 0xFF000000u) | op | (b1 << 8) | (b2 << 16);
+  r.w[7] = (r.w[7] & 0xFFFFu) | (k << 16);
+  return r;
+}
+
+// Record of an instruction from the opcode (and CB sub-opcode) alone.
+__host__ __device__ constexpr Rec decode_base(uint32_t idx) {
+  return pack(idx >= 256u ? decode_cb(idx - 256u) : decode_op(idx));
+}
+
+// Record of the instruction whose first three bytes are op, b1, b2.
+__host__ __device__ constexpr Rec decode_insn(uint32_t op, uint32_t b1, uint32_t b2) {
+  return bind_bytes(decode_base(op == 0xCBu ? 256u + b1 : op), op, b1, b2);
 }
 
 }  // namespace gbx

@@ -45,8 +45,7 @@ struct DecTable {
 };
 constexpr DecTable make_dec_table() {
   DecTable t{};
-  for (uint32_t i = 0; i < 256; ++i) t.e[i] = decode_op(i);
-  for (uint32_t i = 0; i < 256; ++i) t.e[256 + i] = decode_cb(i);
+  for (uint32_t i = 0; i < 512; ++i) t.e[i] = decode_base(i);
   return t;
 }
 __constant__ DecTable kDec = make_dec_table();
@@ -119,8 +118,8 @@ struct Lane {
   const uint8_t* rom;              // ROM buffer (flat)
   uint32_t rom_len;
 
-  // CPU: w0 = B C D E (B in bits 31-24), w1 = H L - A (A in bits 7-0)
-  uint32_t pc, sp, f, w0, w1;
+  // CPU: w0 = B C D E (B in bits 31-24), w1 = H L F A (A in bits 7-0)
+  uint32_t pc, sp, w0, w1;
   uint32_t ime, ime_delay, halted;
   // hot IO registers (byte values); FF04 and the STAT mode/coincidence bits
   // are derived from the timer and PPU position (ff04_val, stat_val)
@@ -161,8 +160,9 @@ struct Lane {
     return Ref8{rm, (addr << kEnvBlockShift) | lane, 0};
   }
 
-  // -- register file (w0 = B C D E, w1 = H L - A) -------------------------------
+  // -- register file (w0 = B C D E, w1 = H L F A) -------------------------------
   __device__ uint32_t a() const { return w1 & 0xFFu; }
+  __device__ uint32_t f() const { return (w1 >> 8) & 0xF0u; }
 
   // -- cartridge windows (reference read8 ROM/RAM branches, :565-656) ----------
   __device__ static int clamp_bank(int bank, int count, int mask) {
@@ -645,9 +645,7 @@ struct Lane {
   // Fetch + decode through the bus (code in RAM, window edges, open bus).
   __device__ Rec fetch_slow() const {
     const uint32_t b0 = read8(pc), b1 = read8(pc + 1u), b2 = read8(pc + 2u);
-    Rec r = kDec.e[b0 == 0xCBu ? 256u + b1 : b0];
-    r.w0 |= b0 | (b1 << 8) | (b2 << 16);
-    return r;
+    return bind_bytes(kDec.e[b0 == 0xCBu ? 256u + b1 : b0], b0, b1, b2);
   }
 };
 
@@ -674,15 +672,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   L.rcs = make_rsrc(s.cs + (size_t)blk * (kCartStateStride * kEnvBlock),
                     kCartStateStride * kEnvBlock * 4);
   const rsrc_t rcnt = make_rsrc(s.cnt + (size_t)blk * (2 * kEnvBlock), 2 * kEnvBlock * 8);
-  const uint4* recs = in_vgpr(reinterpret_cast<const uint4*>(s.recs));
+  const uint4* recs = in_vgpr(reinterpret_cast<const uint4*>(s.recs));  // 4 per record
 
   // ---- load (cpu_step_builder.py:930-967) ---------------------------------
   L.pc = (uint32_t)L.SC(F_PC) & 0xFFFFu;
   L.sp = (uint32_t)L.SC(F_SP) & 0xFFFFu;
-  L.f = (uint32_t)L.SC(F_F) & 0xF0u;
   L.w0 = (((uint32_t)L.SC(F_B) & 0xFFu) << 24) | (((uint32_t)L.SC(F_C) & 0xFFu) << 16) |
          (((uint32_t)L.SC(F_D) & 0xFFu) << 8) | ((uint32_t)L.SC(F_E) & 0xFFu);
   L.w1 = (((uint32_t)L.SC(F_H) & 0xFFu) << 24) | (((uint32_t)L.SC(F_L) & 0xFFu) << 16) |
+         (((uint32_t)L.SC(F_F) & 0xF0u) << 8) |
          ((uint32_t)L.SC(F_A) & 0xFFu);
   L.ime = (uint32_t)L.SC(F_IME);
   L.ime_delay = (uint32_t)L.SC(F_IME_DELAY);
@@ -752,8 +750,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   constexpr bool dbg = kDbg;
 
   // record of the instruction at pc (valid when rv)
-  uint4 rec = uint4{0u, 0u, 0u, 0u};
+  Rec rec{};
   bool rv = false;
+  auto load_rec = [&](uint32_t i) {
+    const uint4* p = recs + (size_t)i * 4u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 q = p[k];
+      rec.w[4 * k] = q.x;
+      rec.w[4 * k + 1] = q.y;
+      rec.w[4 * k + 2] = q.z;
+      rec.w[4 * k + 3] = q.w;
+    }
+  };
 
   // One exit: the frame count reached or the env trapped (a trap freezes
   // the env for the rest of the launch, misc.py:42-56).
@@ -770,13 +779,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       // ---- fetch + decode ------------------------------------------------------
       const uint32_t pc = L.pc;
       if (!rv) {
-        if (L.rec_ok(pc)) rec = recs[L.rec_index(pc)];
-        else {
-          const Rec r = L.fetch_slow();
-          rec = uint4{r.w0, r.w1, r.w2, r.w3};
-        }
+        if (L.rec_ok(pc)) load_rec(L.rec_index(pc));
+        else rec = L.fetch_slow();
       }
-      op = rec.x & 0xFFu;
+      op = rec.w[0] & 0xFFu;
       if (dbg) {  // debug traps before execution: the instruction does not run
         if (dbg_trap_pc && pc == dbg_trap_pc) {
           trap = 1; trap_pc = (int)pc; trap_op = (int)op; trap_kind = 5;
@@ -786,16 +792,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       }
       if (!trap) {
       ExecIn in;
-      in.rec = Rec{rec.x, rec.y, rec.z, rec.w};
       in.w0 = L.w0;
       in.w1 = L.w1;
-      in.f = L.f;
-      in.sp = L.sp;
-      in.pc = pc;
-      in.ra = operand_address(in.rec, L.w0, L.w1, L.sp);
+      in.x1 = (L.sp << 16) | pc;
+      in.ra = operand_address(rec, L.w0, L.w1, in.x1);
 
       // ---- bus reads ------------------------------------------------------------
-      const uint32_t nr = (rec.z >> 16) & 3u;
+      const uint32_t nr = ubfe(rec.w[7], 8, 2);
       in.rd0 = 0;
       in.rd1 = 0;
       if (nr) {
@@ -818,10 +821,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       }
 
       // ---- execute (gbx_exec.h) -------------------------------------------------
-      const ExecOut o = exec_insn(in);
+      const ExecOut o = exec_insn(rec, in);
       L.w0 = o.w0;
       L.w1 = o.w1;
-      L.f = o.f;
       L.sp = o.sp;
       cycles = (int)o.cycles;
       wn = o.wn;
@@ -829,19 +831,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       wv0 = o.wv0;
       wa1 = o.wa1;
       wv1 = o.wv1;
-      L.ime = o.ime_set ? o.ime_on : L.ime;
-      L.ime_delay = o.ime_set ? 0u : L.ime_delay;
-      L.halted = o.halt ? 1u : L.halted;
-      if ((o.trap != 0u) & (trap == 0)) {  // misc.py:42-56: freeze the env, pc unchanged
-        trap = 1;
-        trap_pc = (int)pc;
-        trap_op = (int)op;
-        trap_kind = 1;
+      if (o.misc) {  // DI EI RETI HALT, illegal opcodes
+        if (o.misc & 1u) {
+          L.ime = (o.misc >> 1) & 1u;
+          L.ime_delay = 0;
+        }
+        if (o.misc & 4u) L.halted = 1;
+        if (o.misc & 8u) {  // misc.py:42-56: freeze the env, pc unchanged
+          trap = 1;
+          trap_pc = (int)pc;
+          trap_op = (int)op;
+          trap_kind = 1;
+        }
       }
       L.pc = o.npc;
       // fetch the next record while the writes, timer and PPU run
       rv = L.rec_ok(o.npc);
-      rec = recs[rv ? L.rec_index(o.npc) : 0u];
+      load_rec(rv ? L.rec_index(o.npc) : 0u);
       }
     } else {
       cycles = L.halt_cycles(cframe);
@@ -956,7 +962,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       o[0] = (float)(L.pc & 0xFFFFu) / 65535.0f;
       o[1] = (float)(L.sp & 0xFFFFu) / 65535.0f;
       o[2] = (float)a_ / 255.0f;
-      o[3] = (float)L.f / 255.0f;
+      o[3] = (float)L.f() / 255.0f;
       o[4] = (float)b_ / 255.0f;
       o[5] = (float)c_ / 255.0f;
       o[6] = (float)d_ / 255.0f;
@@ -988,7 +994,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   L.SC(F_E) = (int32_t)e_;
   L.SC(F_H) = (int32_t)h_;
   L.SC(F_L) = (int32_t)l_;
-  L.SC(F_F) = (int32_t)(L.f & 0xF0u);
+  L.SC(F_F) = (int32_t)L.f();
   st64(0, instr);
   st64(1, cyc);
   L.SC(F_CYCLE_IN_FRAME) = cframe;

@@ -23,39 +23,55 @@ static inline uint32_t perm_b32(uint32_t s0, uint32_t s1, uint32_t sel) {
   }
   return r;
 }
-#define __builtin_amdgcn_perm perm_b32
+#define GBX_EXEC_HOST_OPS
+namespace gbx {
+static inline uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) { return perm_b32(s0, s1, sel); }
+// V_BFE_U32 / V_BFE_I32: offset and width from their low 5 bits
+static inline uint32_t ubfe(uint32_t v, uint32_t off, uint32_t width) {
+  off &= 31u;
+  width &= 31u;
+  return width == 0 ? 0u : (v >> off) & ((1u << width) - 1u);
+}
+static inline uint32_t sbfe(uint32_t v, uint32_t off, uint32_t width) {
+  const uint32_t u = ubfe(v, off, width);
+  width &= 31u;
+  return (width != 0 && (u >> (width - 1)) & 1u) ? u | ~((1u << width) - 1u) : u;
+}
+template <int pos>
+static inline uint32_t bit_mask(uint32_t w) { return 0u - ((w >> pos) & 1u); }
+static inline uint32_t add_u16x2(uint32_t a, uint32_t b) {
+  return ((a + b) & 0xFFFFu) | (((a >> 16) + (b >> 16)) << 16);
+}
+}  // namespace gbx
 
 #include "../../gbxcule_amd/csrc/gbx_exec.h"
 
 extern "C" {
 
-// out: 4 words of the record for the instruction bytes op, b1, b2
+// out: the 16 words of the record for the instruction bytes op, b1, b2
 void harness_decode(uint32_t op, uint32_t b1, uint32_t b2, uint32_t* out) {
   const gbx::Rec r = gbx::decode_insn(op, b1, b2);
-  out[0] = r.w0;
-  out[1] = r.w1;
-  out[2] = r.w2;
-  out[3] = r.w3;
+  for (int k = 0; k < gbx::kRecWords; ++k) out[k] = r.w[k];
 }
 
-// in: rec[4], w0, w1, f, sp, pc, rd0, rd1 (11 words); the operand address is
-// computed here.  out: ra, w0, w1, f, sp, npc, cycles, wn, wa0, wv0, wa1, wv1,
-// ime_set, ime_on, halt, trap (16 words).
+// in: rec[16], w0, w1 (H L F A), sp, pc, rd0, rd1 (22 words); the operand
+// address is computed here.  out: ra, w0, w1, sp, npc, cycles, wn, wa0,
+// wv0, wa1, wv1, misc (12 words).
 void harness_exec(const uint32_t* in, uint32_t* out) {
+  gbx::Rec r{};
+  for (int k = 0; k < gbx::kRecWords; ++k) r.w[k] = in[k];
+  const uint32_t* v = in + gbx::kRecWords;
   gbx::ExecIn e{};
-  e.rec = gbx::Rec{in[0], in[1], in[2], in[3]};
-  e.w0 = in[4];
-  e.w1 = in[5];
-  e.f = in[6];
-  e.sp = in[7];
-  e.pc = in[8];
-  e.rd0 = in[9];
-  e.rd1 = in[10];
-  e.ra = gbx::operand_address(e.rec, e.w0, e.w1, e.sp);
-  const gbx::ExecOut o = gbx::exec_insn(e);
-  const uint32_t v[16] = {e.ra, o.w0, o.w1, o.f, o.sp, o.npc, o.cycles, o.wn, o.wa0,
-                          o.wv0, o.wa1, o.wv1, o.ime_set, o.ime_on, o.halt, o.trap};
-  for (int k = 0; k < 16; ++k) out[k] = v[k];
+  e.w0 = v[0];
+  e.w1 = v[1];
+  e.x1 = (v[2] << 16) | v[3];
+  e.rd0 = v[4];
+  e.rd1 = v[5];
+  e.ra = gbx::operand_address(r, e.w0, e.w1, e.x1);
+  const gbx::ExecOut o = gbx::exec_insn(r, e);
+  const uint32_t res[12] = {e.ra, o.w0, o.w1, o.sp, o.npc, o.cycles, o.wn, o.wa0,
+                            o.wv0, o.wa1, o.wv1, o.misc};
+  for (int k = 0; k < 12; ++k) out[k] = res[k];
 }
 
 }  // extern "C"

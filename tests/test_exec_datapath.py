@@ -7,8 +7,8 @@ immediates), so the bytes the datapath reads and writes are plain memory
 and the expected values come from the oracle's memory image.  The oracle
 runs exactly one instruction per env (debug max-instruction trap); the
 registers, F, SP, next pc, IME/HALT/trap and every byte of memory must then
-equal what the datapath produced.  Cycle counts are covered by the GPU
-parity tests, which compare cycle counters after whole frames.
+equal what the datapath produced.  The datapath's cycle count must match
+the public opcode table, taken or not taken as F decides.
 """
 
 from __future__ import annotations
@@ -72,6 +72,26 @@ def _states(rng, n):
     return r
 
 
+def _expected_cycles(op: int, f: int) -> int:
+    """Opcode-table cycles of op (0x100 | cb for CB) with flags f; 0 for a trap."""
+    from .test_oracle_programs import LEGAL, table_cycles
+
+    if op & 0x100:
+        cb = op & 0xFF
+        return 8 if cb & 7 != 6 else 12 if cb >> 6 == 1 else 16
+    if op == 0x76:  # HALT
+        return 4
+    if op not in LEGAL:  # STOP and the unused opcodes trap
+        return 0
+    taken, not_taken = table_cycles(op)
+    if op in (0x20, 0x28, 0x30, 0x38, 0xC0, 0xC8, 0xD0, 0xD8, 0xC2, 0xCA, 0xD2, 0xDA,
+              0xC4, 0xCC, 0xD4, 0xDC):  # fmt: skip
+        cc = (op >> 3) & 3  # NZ Z NC C
+        flag = (f >> 7) & 1 if cc < 2 else (f >> 4) & 1
+        return taken if flag == (cc & 1) else not_taken
+    return taken
+
+
 @pytest.mark.parametrize("seed", [11, 12])
 def test_datapath_matches_oracle(harness, seed):
     rng = np.random.default_rng(seed)
@@ -102,51 +122,55 @@ def test_datapath_matches_oracle(harness, seed):
     m.set_debug(max_instr=1)
     m.step(None, frames=1, release=8)
 
-    rec, inp, out = _arr(4), _arr(11), _arr(16)
+    rec, inp, out = _arr(16), _arr(22), _arr(12)
     bad = []
     for i, op in enumerate(ops):
         opb = 0xCB if op & 0x100 else int(op)
         harness.harness_decode(opb, int(b1[i]), int(b2[i]), rec)
         w0 = (int(regs["b"][i]) << 24) | (int(regs["c"][i]) << 16) | (int(regs["d"][i]) << 8)
         w0 |= int(regs["e"][i])
-        w1 = (int(regs["h"][i]) << 24) | (int(regs["l"][i]) << 16) | int(regs["a"][i])
+        w1 = (int(regs["h"][i]) << 24) | (int(regs["l"][i]) << 16) | (int(regs["f"][i]) << 8)
+        w1 |= int(regs["a"][i])
         sp = int(regs["sp"][i])
         # operand address as the datapath computes it; the bytes there
-        for k in range(4):
+        for k in range(16):
             inp[k] = rec[k]
-        inp[4], inp[5], inp[6], inp[7], inp[8] = w0, w1, int(regs["f"][i]), sp, int(pcs[i])
-        inp[9] = inp[10] = 0
+        inp[16], inp[17], inp[18], inp[19] = w0, w1, sp, int(pcs[i])
+        inp[20] = inp[21] = 0
         harness.harness_exec(inp, out)
         ra = out[0]
-        inp[9] = int(mem0[i, ra & 0xFFFF])
-        inp[10] = int(mem0[i, (ra + 1) & 0xFFFF])
+        inp[20] = int(mem0[i, ra & 0xFFFF])
+        inp[21] = int(mem0[i, (ra + 1) & 0xFFFF])
         harness.harness_exec(inp, out)
         o = list(out)
+        misc = o[11]
         want = {
             "a": o[2] & 0xFF, "b": o[1] >> 24, "c": (o[1] >> 16) & 0xFF, "d": (o[1] >> 8) & 0xFF,
-            "e": o[1] & 0xFF, "h": o[2] >> 24, "l": (o[2] >> 16) & 0xFF, "f": o[3], "sp": o[4],
-            "pc": o[5],
+            "e": o[1] & 0xFF, "h": o[2] >> 24, "l": (o[2] >> 16) & 0xFF, "f": (o[2] >> 8) & 0xFF,
+            "sp": o[3], "pc": o[4],
         }  # fmt: skip
-        ime = o[13] if o[12] else int(regs["ime"][i])
-        want["ime"] = ime
-        want["halted"] = o[14]
+        want["ime"] = (misc >> 1) & 1 if misc & 1 else int(regs["ime"][i])
+        want["halted"] = (misc >> 2) & 1
+        cyc = _expected_cycles(int(op), int(regs["f"][i]))
+        if o[5] != cyc:
+            bad.append(f"op {op:#05x}: cycles datapath={o[5]} table={cyc}")
         for name, v in want.items():
             got = int(m.field(name)[i])
             if got != v:
                 bad.append(f"op {op:#05x}: {name} datapath={v:#x} oracle={got:#x}")
         exp = mem0[i].copy()
-        if o[7] > 2 or any(x > 0xFF for x in (o[9], o[11])):
-            bad.append(f"op {op:#05x}: bad write list {o[7:12]}")
+        if o[6] > 2 or any(x > 0xFF for x in (o[8], o[10])):
+            bad.append(f"op {op:#05x}: bad write list {o[6:11]}")
             continue
-        for k in range(o[7]):
-            a, v = (o[8], o[9]) if k == 0 else (o[10], o[11])
+        for k in range(o[6]):
+            a, v = (o[7], o[8]) if k == 0 else (o[9], o[10])
             exp[a & 0xFFFF] = v
         if not np.array_equal(exp, m.mem[i]):
             d = np.nonzero(exp != m.mem[i])[0]
             bad.append(f"op {op:#05x}: memory differs at {[hex(x) for x in d[:4]]}")
         trapped = int(m.field("trap_kind")[i]) == 1
-        if bool(o[15]) != trapped or (trapped and op not in ILLEGAL | {0x10}):
-            bad.append(f"op {op:#05x}: trap datapath={o[15]} oracle kind={m.field('trap_kind')[i]}")
+        if bool((misc >> 3) & 1) != trapped or (trapped and op not in ILLEGAL | {0x10}):
+            bad.append(f"op {op:#05x}: trap datapath={misc >> 3} oracle kind={m.field('trap_kind')[i]}")
     assert not bad, f"{len(bad)} mismatches:\n" + "\n".join(bad[:30])
 
 
@@ -161,7 +185,7 @@ def test_record_cycles_and_lengths_match_opcode_table(harness):
     opcode table (the same table the oracle's cycle-count test uses)."""
     from .test_oracle_programs import LEGAL, table_cycles
 
-    rec = _arr(4)
+    rec = _arr(16)
     for op in LEGAL:
         harness.harness_decode(op, 0, 0, rec)
         taken, not_taken = ((rec[0] >> 26) & 7) * 4, (rec[0] >> 29) * 4
