@@ -69,7 +69,7 @@ hipError_t dalloc(T** p, size_t count) {
 // 0xFF that an unmapped ROM bank reads (open bus).
 constexpr int64_t kOpenBusBytes = 0x4000;
 
-// Pre-decoded instruction records for the step kernel's fetch: one 128-bit
+// Pre-decoded instruction records for the step kernel's fetch: one 512-bit
 // record (gbx_decode.h) per byte of the ROM buffer, built from that byte and
 // the next two bytes of the same image.  Bytes past the end of an image read
 // as 0; the kernel only uses a record when all three instruction bytes lie

@@ -104,6 +104,16 @@ __device__ __forceinline__ T* in_vgpr(T* p) {
   return reinterpret_cast<T*>(((uint64_t)in_vgpr((uint32_t)(a >> 32)) << 32) | in_vgpr((uint32_t)a));
 }
 
+// Loads through flat pointers that are known to be device (global) memory,
+// issued as global loads: the compiler then counts them exactly in vmcnt and
+// can wait for one load while later ones stay in flight (a flat load could
+// also be an LDS access, so waits on flat loads drain every load).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ T ld_global(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+
 // ---------------------------------------------------------------------------
 // Per-lane machine.  Everything here is scalarized into VGPRs.
 // ---------------------------------------------------------------------------
@@ -256,7 +266,7 @@ struct Lane {
   }
   __device__ uint32_t read8(uint32_t addr) const {
     const uint32_t x = fold(addr);
-    return bus_fix(x, *bus_ptr(x));
+    return bus_fix(x, ld_global(bus_ptr(x)));
   }
   __device__ void set_if(uint32_t v) {
     ifr = v;
@@ -756,11 +766,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     const uint4* p = recs + (size_t)i * 4u;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint4 q = p[k];
-      rec.w[4 * k] = q.x;
-      rec.w[4 * k + 1] = q.y;
-      rec.w[4 * k + 2] = q.z;
-      rec.w[4 * k + 3] = q.w;
+      const u32x4 q = ld_global(reinterpret_cast<const u32x4*>(p + k));
+      rec.w[4 * k] = q[0];
+      rec.w[4 * k + 1] = q[1];
+      rec.w[4 * k + 2] = q[2];
+      rec.w[4 * k + 3] = q[3];
     }
   };
 
@@ -815,7 +825,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           if ((x1 != x0 + 1u) | (x0 < 0x8000u) | (x0 - 0xA000u < 0x2000u) | (x1 - 0xA000u < 0x2000u))
             p1 = L.bus_ptr(x1);
         }
-        const uint32_t v0 = *p0, v1 = *p1;
+        const uint32_t v0 = ld_global(p0), v1 = ld_global(p1);
         in.rd0 = L.bus_fix(x0, v0);
         in.rd1 = L.bus_fix(x1, v1);
       }
