@@ -867,13 +867,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     int svc = 0;
     if (wn >= 1u) L.write8(wa0, wv0);
     if (wn >= 2u) L.write8(wa1, wv1);
-    if (!hiter) {
-      if (dbg && dbg_rst38 && L.pc >= 0xFE00u && !trap) {
-        trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4;
-      }
-      if (!trap) {
-        ninstr += 1;
-        if (dbg) {
+    if (dbg) {
+      if (!hiter) {
+        if (dbg_rst38 && L.pc >= 0xFE00u && !trap) {
+          trap = 1; trap_pc = (int)pc_before; trap_op = (int)op; trap_kind = 4;
+        }
+        if (!trap) {
+          ninstr += 1;
           if (dbg_max_instr > 0 && instr + ninstr - instr_start >= dbg_max_instr) {
             trap = 1; trap_pc = (int)L.pc; trap_op = (int)op; trap_kind = 6;
           } else if (dbg_watch && watch_read() != watch_val) {
@@ -881,8 +881,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           }
         }
       }
+    } else {
+      ninstr += (uint32_t)((!hiter) & (trap == 0));
     }
-    if (!trap) {
+    // Fast path: when no timer edge or reload, no scanline wrap, no LCD
+    // switch, no pending interrupt, no remap, no RTC second and no frame end
+    // fall inside this step, the sequence below reduces to DIV, the scanline
+    // position and the cycle counters advancing; one test covers all of it.
+    const uint32_t lc_now = L.lcdc;
+    const uint32_t ucyc = (uint32_t)cycles;
+    const bool lcd_on = (lc_now & 0x80u) != 0u;
+    bool fast = (trap == 0) & (L.pend == 0u) & (((L.div & 0xFFFFu & L.tmask) + ucyc) <= L.tmask) &
+                (L.ime_delay == 0u) & ((L.ie & L.ifr & 0x1Fu) == 0u) & (L.map_changed == 0u) &
+                (((lcdc_prev ^ lc_now) & 0x80u) == 0u) & (cframe + cycles < kCyclesPerFrame) &
+                (lcd_on ? (L.scan + ucyc < (uint32_t)kCyclesPerLine)
+                        : ((L.scan | L.ly | L.wl | L.lym) == 0u));
+    if (kMbc == MBC_MBC3)
+      fast = fast & ((L.rtc_halt != 0u) | ((L.rtc_sub >= 0) & (L.rtc_sub + cycles < kRtcCyclesPerSecond) &
+                                           (L.rtc_dirty == 0u)));
+    if (fast) {
+      L.div = (L.div + ucyc) & 0xFFFFu;
+      L.scan = lcd_on ? L.scan + ucyc : 0u;
+      L.stat_fresh = 0;
+      L.lyc_pp = L.lyc;
+      L.lcd_pp = lc_now & 0x80u;
+      if (kMbc == MBC_MBC3) L.rtc_sub += L.rtc_halt ? 0 : cycles;
+      ncyc += ucyc;
+      cframe += cycles;
+    } else if (!trap) {
       L.timer_tick(cycles);
       if (!hiter & (L.ime_delay != 0u)) {
         L.ime = 1;
