@@ -260,8 +260,14 @@ struct Lane {
   }
   // Value the bus returned for a load v issued at bus_ptr(x).
   __device__ uint32_t bus_fix(uint32_t x, uint32_t v) const {
-    if (x - 0xA000u < 0x2000u) v = cart_fix(v);
-    if (io_derived(x)) v = io_fix(x, v);
+    const bool cart = x - 0xA000u < 0x2000u;
+    if (mbc == MBC_MBC3) {
+      if (cart) v = cart_fix(v);
+    } else {
+      v = (cart & !ram_ok) ? 0xFFu : v;  // no RTC: disabled RAM reads 0xFF
+    }
+    v = x == 0xFF04u ? ff04_val() : v;
+    if (x == 0xFF41u) v = stat_val();
     return v;
   }
   __device__ uint32_t read8(uint32_t addr) const {
@@ -522,11 +528,29 @@ struct Lane {
       io_write(x, v);
     }
   }
+  // A write that is not a plain store to the env's memory: MBC registers,
+  // cartridge RAM, IO bytes with side effects.
+  __device__ static bool write_is_special(uint32_t x) {
+    return (x < 0x8000u) | (x - 0xA000u < 0x2000u) | io_special(x);
+  }
   __device__ void write8(uint32_t addr, uint32_t v) {
     const uint32_t x = fold(addr);
-    const bool special = (x < 0x8000u) | (x - 0xA000u < 0x2000u) | io_special(x);
-    if (!special) M(x) = v;
+    if (!write_is_special(x)) M(x) = v;
     else write_special(x, v);
+  }
+  // The instruction's bus writes, in order (n = 0, 1 or 2).  When none is
+  // special both are plain stores without a branch; a lane with one write
+  // stores its first byte twice.
+  __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1) {
+    const uint32_t x0 = fold(a0), x1 = fold(a1);
+    const bool two = n >= 2u;
+    if (write_is_special(x0) | (two & write_is_special(x1))) {
+      write8(a0, v0);
+      if (two) write8(a1, v1);
+    } else {
+      M(x0) = v0;
+      M(two ? x1 : x0) = two ? v1 : v0;
+    }
   }
 
   // -- PPU line bookkeeping (cpu_step_builder.py:421-524, 1406-1500) -----------
@@ -574,7 +598,9 @@ struct Lane {
       total -= kCyclesPerLine;
       const uint32_t pl = ly;
       if (pl < (uint32_t)kScreenH && (lc & 0x20u) && pl >= wy) wl += 1;
-      ly = (ly + 1u) % (uint32_t)kLinesPerFrame;
+      uint32_t nl = ly + 1u;
+      if (nl >= (uint32_t)kLinesPerFrame) nl %= (uint32_t)kLinesPerFrame;
+      ly = nl;
       if (ly == 0) wl = 0;
       lym = ly;
       // ppu_update_stat_irq with mode 0 or 1
@@ -865,8 +891,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
 
     // ---- write phase, debug checks, timer, PPU, interrupt check --------------
     int svc = 0;
-    if (wn >= 1u) L.write8(wa0, wv0);
-    if (wn >= 2u) L.write8(wa1, wv1);
+    if (wn) L.write_bus(wn, wa0, wv0, wa1, wv1);
     if (dbg) {
       if (!hiter) {
         if (dbg_rst38 && L.pc >= 0xFE00u && !trap) {
@@ -894,8 +919,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     bool fast = (trap == 0) & (L.pend == 0u) & (((L.div & 0xFFFFu & L.tmask) + ucyc) <= L.tmask) &
                 (L.ime_delay == 0u) & ((L.ie & L.ifr & 0x1Fu) == 0u) & (L.map_changed == 0u) &
                 (((lcdc_prev ^ lc_now) & 0x80u) == 0u) & (cframe + cycles < kCyclesPerFrame) &
-                (lcd_on ? (L.scan + ucyc < (uint32_t)kCyclesPerLine)
-                        : ((L.scan | L.ly | L.wl | L.lym) == 0u));
+                ((lcd_on & (L.scan + ucyc < (uint32_t)kCyclesPerLine)) |
+                 (!lcd_on & ((L.scan | L.ly | L.wl | L.lym) == 0u)));
     if (kMbc == MBC_MBC3)
       fast = fast & ((L.rtc_halt != 0u) | ((L.rtc_sub >= 0) & (L.rtc_sub + cycles < kRtcCyclesPerSecond) &
                                            (L.rtc_dirty == 0u)));
