@@ -597,21 +597,20 @@ struct Lane {
     while (total >= (uint32_t)kCyclesPerLine) {
       total -= kCyclesPerLine;
       const uint32_t pl = ly;
-      if (pl < (uint32_t)kScreenH && (lc & 0x20u) && pl >= wy) wl += 1;
+      wl += (uint32_t)((pl < (uint32_t)kScreenH) & ((lc & 0x20u) != 0u) & (pl >= wy));
       uint32_t nl = ly + 1u;
       if (nl >= (uint32_t)kLinesPerFrame) nl %= (uint32_t)kLinesPerFrame;
       ly = nl;
-      if (ly == 0) wl = 0;
+      wl = ly == 0u ? 0u : wl;
       lym = ly;
-      // ppu_update_stat_irq with mode 0 or 1
-      const uint32_t mode = ly >= (uint32_t)kScreenH ? 1u : 0u;
-      const uint32_t coin = ly == lyc ? 1u : 0u;
-      const uint32_t cur = (mode == 0 ? 1u : 0u) | (mode == 1 ? 2u : 0u) | (coin << 3);
+      // ppu_update_stat_irq with mode 0 or 1: bit0 mode 0, bit1 mode 1, bit3 LY == LYC
+      const uint32_t vb = ly >= (uint32_t)kScreenH ? 1u : 0u;
+      const uint32_t cur = (1u << vb) | ((ly == lyc ? 1u : 0u) << 3);
       const uint32_t en = (stat_full >> 3) & 0xFu;  // bit0 mode0, 1 mode1, 2 mode2, 3 lyc
-      if (en & cur & ~(prev & 0xFu)) ifr |= 0x02u;
+      ifr |= (uint32_t)((en & cur & ~(prev & 0xFu)) != 0u) << 1;
       prev = cur;
-      if (pl == 143u && ly == 144u) ifr |= 0x01u;
-      if (ly < (uint32_t)kScreenH) latch_env0();
+      ifr |= (uint32_t)((pl == 143u) & (ly == 144u));
+      if ((e == 0u) & (ly < (uint32_t)kScreenH)) latch_env0();
     }
     scan = total;
     M(0xFF44) = lym;
