@@ -38,7 +38,8 @@
 // w9  SW1   writeback selector of W1 (F always takes the new flags)
 // w10 FL    [0:7] flags taken from the computed Z/H/C  [8:15] flags not forced to 0
 //           [16:23] flags inverted last  [24] IME write  [25] IME value  [26] HALT
-//           [27] trap  [28] SP takes the 16-bit sum  [29] DAA
+//           [27] trap  [28] LY poll loop starts here (set by the record builder)
+//           [29] SP takes the 16-bit sum  [30] DAA
 // w11 TN    not taken [0:4] cycles [5:6] bus writes [7:9] SP delta (signed);
 //           taken the same at [16:25]
 // w12 TW    [0:4] branch test bit of W1 ^ TW  [8:15] its inversion mask
@@ -47,7 +48,9 @@
 //           [8:15] subtract mask (0xFF: y complemented)  [16:31] flag-source selector
 // w14 SHW   [0:15] shifter funnel selector  [16:20] funnel right shift  [24:31] adder
 //           result mask (0xFF)
-// w15 DW    bus write addresses: operand address + DW, per 16-bit half (wrapping)
+// w15 DW    bus write addresses: operand address + DW, per 16-bit half (wrapping);
+//           for a poll-loop start (FL bit 28, a read): [0:7] the CP constant,
+//           [8:9] the JR condition (0 NZ, 1 Z, 2 NC, 3 C)
 #pragma once
 #include <stdint.h>
 
@@ -430,7 +433,7 @@ __host__ __device__ constexpr Rec pack(Dec d) {
   r.w[8] = d.sw0;
   r.w[9] = d.sw1;
   r.w[10] = d.E | (d.M << 8) | (d.X << 16) | (d.ime_set << 24) | (d.ime_on << 25) |
-            (d.halt << 26) | (d.trap << 27) | (d.spw << 28) | (d.daa << 29);
+            (d.halt << 26) | (d.trap << 27) | (d.spw << 29) | (d.daa << 30);
   // a non-jump is never "taken": its fields live in the not-taken half
   const uint32_t tk = d.cond == C_NEVER ? 0u : tn_half(d.cyc, d.wn, d.dsp);
   r.w[11] = tn_half(d.cond == C_NEVER ? d.cyc : d.cycnt, d.wn_nt, d.dsp_nt) | (tk << 16);
@@ -442,6 +445,22 @@ __host__ __device__ constexpr Rec pack(Dec d) {
 }
 
 __host__ __device__ constexpr uint32_t sext8(uint32_t v) { return (uint32_t)(int32_t)(int8_t)(v & 0xFFu); }
+
+// LY poll loop: the six bytes at an address are LDH A,(44); CP d8; JR cc,-6
+// (jumping back to the LDH).  The record builder marks such an LDH (FL bit
+// 28, DW = d8 | cc << 8); while LY stays the same every pass through the
+// loop leaves the same A and F, so the step kernel may advance whole passes
+// at once (32 cycles, 3 instructions each) up to the next event.
+constexpr uint32_t kPollFlag = 1u << 28;
+__host__ __device__ constexpr bool poll_loop_at(const uint8_t* p) {
+  return p[0] == 0xF0u && p[1] == 0x44u && p[2] == 0xFEu &&
+         (p[4] == 0x20u || p[4] == 0x28u || p[4] == 0x30u || p[4] == 0x38u) && p[5] == 0xFAu;
+}
+__host__ __device__ constexpr Rec mark_poll_loop(Rec r, const uint8_t* p) {
+  r.w[10] |= kPollFlag;
+  r.w[15] = p[3] | (((uint32_t)(p[4] - 0x20u) >> 3) << 8);
+  return r;
+}
 
 // Bind the instruction bytes op, b1, b2 into a record decoded from the
 // opcode alone: the bytes go into w0, K into KW per the record's KMode.

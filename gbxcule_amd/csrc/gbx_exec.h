@@ -50,7 +50,7 @@ struct ExecOut {
   uint32_t w0, w1, sp, npc;
   uint32_t cycles;
   uint32_t wn, wa0, wv0, wa1, wv1;  // bus writes, in order
-  uint32_t misc;                    // [0] IME write [1] IME value [2] HALT [3] trap
+  uint32_t misc;                    // [0] IME write [1] IME value [2] HALT [3] trap [4] poll loop
 };
 
 // Operand address of the bus operand (cpu_templates/loads.py address modes):
@@ -98,7 +98,7 @@ __device__ __forceinline__ ExecOut exec_insn(const Rec& r, const ExecIn& in) {
   const uint32_t t16 = sum ^ A16 ^ B16;
   const uint32_t fsv = t8 | perm(t16, XW, CIW >> 16);
   uint32_t cf = ubfe(fsv, 8, 1);
-  if (FL & (1u << 29)) {  // DAA (alu.py:897-950)
+  if (FL & (1u << 30)) {  // DAA (alu.py:897-950)
     const uint32_t nf = (W1 >> 14) & 1u, hf = (W1 >> 13) & 1u, cin = (W1 >> 12) & 1u;
     const bool dlo = nf ? hf != 0u : (hf != 0u || (x & 15u) > 9u);
     const bool dhi = nf ? cin != 0u : (cin != 0u || x > 0x99u);
@@ -126,7 +126,7 @@ __device__ __forceinline__ ExecOut exec_insn(const Rec& r, const ExecIn& in) {
   const uint32_t dsp = sbfe(sel, 7, 3);
   const uint32_t seq = ((X1 & 0xFFFFu) + ubfe(R0, 24, 2)) & 0xFFFFu;
   o.npc = taken ? v16 : seq;
-  const uint32_t mspw = bit_mask<28>(FL);
+  const uint32_t mspw = bit_mask<29>(FL);
   o.sp = (v16 & mspw) | (((X1 >> 16) + dsp) & 0xFFFFu & ~mspw);
 
   // ---- bus writes: the result to the operand, or two bytes (PUSH, CALL, RST,
@@ -137,7 +137,7 @@ __device__ __forceinline__ ExecOut exec_insn(const Rec& r, const ExecIn& in) {
   const uint32_t WV = perm(U, seq, TW >> 16);
   o.wv0 = WV & 0xFFu;
   o.wv1 = ubfe(WV, 8, 8);
-  o.misc = ubfe(FL, 24, 4);
+  o.misc = ubfe(FL, 24, 5);
   return o;
 }
 

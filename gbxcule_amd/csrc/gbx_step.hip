@@ -645,6 +645,29 @@ struct Lane {
   // the first 4-cycle step that reaches the nearest of those.  A request
   // already pending (a launch that ended before its interrupt check, or
   // imported state) wakes the CPU after the first 4 cycles.
+  // Whole passes of an LY poll loop (LDH A,(44); CP d8; JR cc,back; 32
+  // cycles) that can be taken in one step from the LDH that just read ly:
+  // 0 unless the jump back is taken.  The reference runs the loop one
+  // instruction at a time with the timer, PPU, interrupt check and frame
+  // count after each; nothing it observes changes before the next scanline
+  // (LY), TIMA overflow, frame end or interrupt service, so passes are taken
+  // up to the nearest of those, the last one ending at or before it.
+  __device__ int poll_passes(uint32_t dw, uint32_t ly, int cframe) const {
+    const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
+    const bool z = ly == d8, c = ly < d8;
+    const bool back = cc == 0u ? !z : cc == 1u ? z : cc == 2u ? !c : c;
+    if (!back || ime_delay != 0u || (ime != 0u && (ie & ifr & 0x1Fu) != 0u)) return 0;
+    int d = kCyclesPerFrame - cframe;
+    if (lcdc & 0x80u) d = min(d, kCyclesPerLine - (int)scan);
+    if (pend) {
+      d = min(d, max((int)delay, 1));
+    } else if (tac & 4u) {
+      const int period = 1 << (div_bit(tac) + 1);
+      const int edge = period - (int)(div & (uint32_t)(period - 1));
+      d = min(d, edge + (int)(255u - tima) * period);
+    }
+    return d >= 32 ? d / 32 : 0;
+  }
   __device__ int halt_cycles(int cframe) const {
     if (ie & ifr & 0x1Fu) return 4;
     int d = kCyclesPerFrame - cframe;
@@ -866,7 +889,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       wv0 = o.wv0;
       wa1 = o.wa1;
       wv1 = o.wv1;
-      if (o.misc) {  // DI EI RETI HALT, illegal opcodes
+      uint32_t npc = o.npc;
+      if (o.misc) {  // DI EI RETI HALT, illegal opcodes, LY poll loops
         if (o.misc & 1u) {
           L.ime = (o.misc >> 1) & 1u;
           L.ime_delay = 0;
@@ -878,11 +902,27 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           trap_op = (int)op;
           trap_kind = 1;
         }
+        if (!dbg && (o.misc & 16u)) {
+          // LDH A,(44) just read LY into A; if CP d8 / JR cc takes the jump
+          // back, every pass until LY or anything else can change reads the
+          // same LY and leaves the same A and F: advance k whole passes (this
+          // LDH included) in one step.
+          const int k = L.poll_passes(rec.w[15], in.rd0, cframe);
+          if (k > 0) {
+            const uint32_t ly = in.rd0, d8 = rec.w[15] & 0xFFu;
+            const uint32_t f = ((ly == d8) ? 0x80u : 0u) | 0x40u | (((ly & 15u) < (d8 & 15u)) ? 0x20u : 0u) |
+                               ((ly < d8) ? 0x10u : 0u);
+            L.w1 = (L.w1 & 0xFFFF00FFu) | (f << 8);
+            npc = pc;
+            cycles = 32 * k;
+            ninstr += 3u * (uint32_t)k - 1u;
+          }
+        }
       }
-      L.pc = o.npc;
+      L.pc = npc;
       // fetch the next record while the writes, timer and PPU run
-      rv = L.rec_ok(o.npc);
-      load_rec(rv ? L.rec_index(o.npc) : 0u);
+      rv = L.rec_ok(npc);
+      load_rec(rv ? L.rec_index(npc) : 0u);
       }
     } else {
       cycles = L.halt_cycles(cframe);
