@@ -74,4 +74,15 @@ void harness_exec(const uint32_t* in, uint32_t* out) {
   for (int k = 0; k < 12; ++k) out[k] = res[k];
 }
 
+// out: [is a poll-loop start, FL word, DW word] of the decoded and marked
+// record at p (6 bytes)
+void harness_poll(const uint8_t* p, uint32_t* out) {
+  gbx::Rec r = gbx::decode_insn(p[0], p[1], p[2]);
+  const bool poll = gbx::poll_loop_at(p);
+  if (poll) r = gbx::mark_poll_loop(r, p);
+  out[0] = poll ? 1u : 0u;
+  out[1] = r.w[10];
+  out[2] = r.w[15];
+}
+
 }  // extern "C"

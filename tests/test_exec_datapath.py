@@ -44,6 +44,7 @@ def harness(tmp_path_factory):
     u32p = ctypes.POINTER(ctypes.c_uint32)
     lib.harness_decode.argtypes = [ctypes.c_uint32] * 3 + [u32p]
     lib.harness_exec.argtypes = [u32p, u32p]
+    lib.harness_poll.argtypes = [ctypes.c_char_p, u32p]
     return lib
 
 
@@ -197,3 +198,23 @@ def test_record_cycles_and_lengths_match_opcode_table(harness):
         exp = 8 if cb & 7 != 6 else 12 if cb >> 6 == 1 else 16
         assert ((rec[0] >> 26) & 7) * 4 == exp, f"cb {cb:#04x}"
         assert (rec[0] >> 24) & 3 == 2
+
+
+def test_poll_loop_marking(harness):
+    """The record builder marks exactly LDH A,(44); CP d8; JR cc,-6 and
+    stores the compare constant and the jump condition."""
+    out = _arr(3)
+    for cc_op, cc in ((0x20, 0), (0x28, 1), (0x30, 2), (0x38, 3)):
+        harness.harness_poll(bytes([0xF0, 0x44, 0xFE, 0x90, cc_op, 0xFA]), out)
+        assert out[0] == 1 and out[1] & (1 << 28) and out[2] == 0x90 | (cc << 8)
+        # the LDH itself still decodes and executes as an LDH
+        assert (out[1] & ~(1 << 28)) & (0x7F << 24) == 0
+    for bad in (
+        [0xF0, 0x45, 0xFE, 0x90, 0x20, 0xFA],  # not LY
+        [0xF0, 0x44, 0xE6, 0x90, 0x20, 0xFA],  # AND, not CP
+        [0xF0, 0x44, 0xFE, 0x90, 0x18, 0xFA],  # unconditional JR
+        [0xF0, 0x44, 0xFE, 0x90, 0x20, 0xFB],  # jumps elsewhere
+        [0xFA, 0x44, 0xFF, 0xFE, 0x90, 0x20],  # LD A,(a16) form
+    ):
+        harness.harness_poll(bytes(bad), out)
+        assert out[0] == 0 and not out[1] & (1 << 28)

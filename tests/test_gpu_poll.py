@@ -1,0 +1,141 @@
+"""LY poll loops (LDH A,(44); CP d8; JR cc,back) against the oracle.
+
+The step kernel advances whole passes of such a loop in one step up to the
+next scanline, TIMA overflow, frame end or interrupt service.  These carts
+poll with every jump condition while timer, STAT (LYC) and VBlank interrupts
+fire with IME on or off, the LCD is switched off and on, and TIMA runs at
+every rate; state is compared in full after every step.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gbxcule_amd.carts.asm import Asm
+from gbxcule_amd.carts.synth import PROGRAM_ORIGIN, _vectors, finalize_rom, seeded_actions
+from oracle.ref import RefMachine
+
+from ._parity import assert_same_state
+from .conftest import require_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool) -> bytes:
+    """A 32 KiB ROM-only cart whose main loop waits on LY four ways."""
+    rng = np.random.default_rng(seed)
+    rom = bytearray(0x8000)
+    h = Asm(origin=0x0068)
+    for name, counter in (("vbl", 0xDF00), ("stat", 0xDF01), ("timer", 0xDF02)):
+        h.label(name)
+        h.push("AF")
+        h.push("HL")
+        h.ld_rr_d16("HL", counter)
+        h.emit(0x34)  # INC (HL)
+        if name == "stat":  # move LYC on
+            h.ldh_a_a8(0x45)
+            h.alu_d8("ADD", int(rng.integers(5, 40)))
+            h.alu_d8("CP", 154)
+            h.jr("lyc_ok", "C")
+            h.alu_d8("SUB", 154)
+            h.label("lyc_ok")
+            h.ldh_a8_a(0x45)
+        h.pop("HL")
+        h.pop("AF")
+        h.reti()
+    code = h.resolve()
+    rom[0x68 : 0x68 + len(code)] = code
+    _vectors(rom, {0x40: h.labels["vbl"], 0x48: h.labels["stat"], 0x50: h.labels["timer"]})
+
+    a = Asm(origin=PROGRAM_ORIGIN)
+    a.ld_rr_d16("SP", 0xDFF0)
+    a.ld_r_d8("A", int(rng.integers(0, 256)))
+    a.ldh_a8_a(0x06)  # TMA
+    a.ld_r_d8("A", tac)
+    a.ldh_a8_a(0x07)  # TAC
+    a.ld_r_d8("A", int(rng.integers(0, 154)))
+    a.ldh_a8_a(0x45)  # LYC
+    a.ld_r_d8("A", 0x40)
+    a.ldh_a8_a(0x41)  # STAT: LYC interrupt source
+    a.ld_r_d8("A", ie)
+    a.ldh_a8_a(0xFF)
+    a.ld_r_d8("A", 0x00)
+    a.ldh_a8_a(0x0F)
+    if ime:
+        a.ei()
+    a.ld_r_d8("A", 0x91)
+    a.ldh_a8_a(0x40)  # LCD on
+    a.label("loop")
+    lines = [int(x) for x in rng.integers(1, 153, 3)]
+    a.label("w1")  # until LY == 144
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", 144)
+    a.jr("w1", "NZ")
+    a.label("w2")  # while LY == 144
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", 144)
+    a.jr("w2", "Z")
+    a.label("w3")  # while LY < n
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", lines[0])
+    a.jr("w3", "C")
+    a.label("w4")  # until LY < n (wraps through VBlank)
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", lines[1])
+    a.jr("w4", "NC")
+    a.ld_a_a16(0xC000)
+    a.inc_r("A")
+    a.ld_a16_a(0xC000)
+    if lcd_off_frames:
+        a.alu_d8("AND", 0x03)
+        a.jr("loop", "NZ")
+        a.ld_r_d8("A", 0x11)
+        a.ldh_a8_a(0x40)  # LCD off: LY reads 0
+        a.label("w5")  # until LY == n: never, while the LCD is off
+        a.ldh_a_a8(0x44)
+        a.alu_d8("CP", lines[2])
+        a.jr("w5", "NZ")
+    a.jp("loop")
+    code = a.resolve()
+    rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
+    return finalize_rom(rom, "GBXAMD POLL", 0x00, 0x00, 0x00)
+
+
+CASES = [
+    # seed, IME, IE, TAC, LCD-off frames
+    (1, True, 0x07, 0x05, False),
+    (2, True, 0x05, 0x04, False),
+    (3, False, 0x07, 0x07, False),
+    (4, True, 0x03, 0x00, True),
+    (5, True, 0x04, 0x06, True),
+]
+
+
+@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off", CASES)
+def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off):
+    require_gpu()
+    from gbxcule_amd.backend import HipVecBackend
+
+    rom = poll_cart(seed, ime, ie, tac, lcd_off)
+    n, fs, steps = 64, 24, 4
+    dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
+                        stage="emulate_only", bootrom=bootstub)  # fmt: skip
+    ref = RefMachine(n, rom, bootstub)
+    try:
+        dut.reset(seed=seed)
+        ref.step(None, 0, 0, "emulate_only")
+        assert_same_state(dut, ref, step=-1, tag=f"poll{seed}")
+        for k in range(steps):
+            act = seeded_actions(seed, k, n)
+            dut.step(act)
+            ref.step(act, fs, 8, "emulate_only", threads=8)
+            assert_same_state(dut, ref, step=k, tag=f"poll{seed}")
+        mem = ref.mem
+        assert int(mem[0, 0xC000]) > 0  # the loops completed passes
+        if ime and ie & 4 and tac & 4:
+            assert int(mem[0, 0xDF02]) > 0  # timer interrupts were serviced
+        assert int(ref.field("trap_flag").sum()) == 0
+    finally:
+        dut.close()
+        ref.close()
