@@ -157,6 +157,10 @@ struct Lane {
   // frame loop
   int frames_done, release;
   int32_t action;
+  // JOYP: the select bits last written, and the FF00 value for each select
+  // (bytes 0-3 for select 0x00, 0x10, 0x20, 0x30), which changes only when
+  // the frame count passes the release frame
+  uint32_t joyp_sel, joyp_word;
 
   __device__ __forceinline__ Ref32 CS(int slot) const {
     if (__builtin_constant_p(slot)) return Ref32{rcs, lane << 2, (uint32_t)slot << 8};
@@ -376,6 +380,11 @@ struct Lane {
   }
 
   // -- JOYP (cpu_step_builder.py:195-247) ----------------------------------------
+  __device__ void joyp_refresh() {
+    joyp_word = joyp_value(0x00u) | (joyp_value(0x10u) << 8) | (joyp_value(0x20u) << 16) |
+                (joyp_value(0x30u) << 24);
+  }
+  __device__ uint32_t joyp_read(uint32_t sl) const { return ubfe(joyp_word, (sl & 0x30u) >> 1, 8); }
   __device__ uint32_t joyp_value(uint32_t sl) const {
     const bool pressed = frames_done < release;
     uint32_t dpad = 0, btn = 0;
@@ -393,12 +402,13 @@ struct Lane {
   }
 
   // -- bus write (reference write8, cpu_step_builder.py:659-873) ----------------
-  // IO bytes with side effects or a VGPR copy: FF00 02 04-07 0F 40 41 44 45
-  // 46 4A 50 and FFFF.  Every other address below FF80 outside ROM and
+  // IO bytes with side effects or a VGPR copy: FF02 04-07 0F 40 41 44 45 46
+  // 4A 50 and FFFF.  FF00 (JOYP) is a plain store of the joypad value for the
+  // written select bits; every other address below FF80 outside ROM and
   // cartridge RAM is a plain store.
   __device__ static bool io_special(uint32_t x) {
     const uint32_t k = x & 0xFFu;
-    const uint32_t m = k < 32u ? 0x80F5u : (k - 64u < 32u ? 0x10473u : 0u);
+    const uint32_t m = k < 32u ? 0x80F4u : (k - 64u < 32u ? 0x10473u : 0u);
     return (x >= 0xFF00u) & ((k == 0xFFu) | (((m >> (k & 31u)) & 1u) != 0u));
   }
   __device__ void io_write(uint32_t x, uint32_t v) {
@@ -423,11 +433,10 @@ struct Lane {
         k == 0xFFu)
       M(x) = mv;
     switch (k) {
-      case 0x00: {
-        const uint32_t sl = v & 0x30u;
-        SC(F_JOYP_SELECT) = (int32_t)sl;
-        M(0xFF00) = joyp_value(sl);
-      } break;
+      case 0x00:
+        joyp_sel = v & 0x30u;
+        M(0xFF00) = joyp_read(v);
+        break;
       case 0x02:
         if ((v & 0x80u) && (v & 0x01u)) {
           const int idx = SC(F_SERIAL_LEN);
@@ -548,8 +557,13 @@ struct Lane {
       write8(a0, v0);
       if (two) write8(a1, v1);
     } else {
-      M(x0) = v0;
-      M(two ? x1 : x0) = two ? v1 : v0;
+      const bool j0 = x0 == 0xFF00u, j1 = two & (x1 == 0xFF00u);
+      const uint32_t s0 = j0 ? joyp_read(v0) : v0;
+      const uint32_t s1 = two ? (j1 ? joyp_read(v1) : v1) : s0;
+      joyp_sel = j0 ? v0 & 0x30u : joyp_sel;
+      joyp_sel = j1 ? v1 & 0x30u : joyp_sel;
+      M(x0) = s0;
+      M(two ? x1 : x0) = s1;
     }
   }
 
@@ -776,6 +790,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   L.action = args.actions[e];
   L.release = (int)in_vgpr((uint32_t)args.release);
   L.frames_done = 0;
+  L.joyp_sel = (uint32_t)L.SC(F_JOYP_SELECT);
+  L.joyp_refresh();
 
   auto ld64 = [&](uint32_t slot) {
     const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(rcnt, (int)(L.lane << 3), (int)(slot << 9), 0);
@@ -1029,6 +1045,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           }
           cframe = tail;
           ++L.frames_done;
+          L.joyp_refresh();
         } else if (!hiter && !lcdc_prev && (lcdc_now & 0x80u)) {
           L.scan = 0;
           L.ly = 0;
@@ -1037,11 +1054,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           L.stat_fresh = 0;  // STAT and stat_prev follow from scan 0 of line 0
           cframe = 0;
           ++L.frames_done;
+          L.joyp_refresh();
         } else {
           while (cframe >= kCyclesPerFrame && L.frames_done < frames) {
             cframe -= kCyclesPerFrame;
             ++L.frames_done;
           }
+          L.joyp_refresh();
         }
       }
     }
@@ -1103,6 +1122,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   L.SC(F_TRAP_OPCODE) = trap_op;
   L.SC(F_TRAP_KIND) = trap_kind;
   L.SC(F_IME) = (int32_t)L.ime;
+  L.SC(F_JOYP_SELECT) = (int32_t)L.joyp_sel;
   L.SC(F_IME_DELAY) = (int32_t)L.ime_delay;
   L.SC(F_HALTED) = (int32_t)L.halted;
   L.SC(F_DIV_COUNTER) = (int32_t)L.div;
