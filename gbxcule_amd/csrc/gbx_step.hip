@@ -243,8 +243,10 @@ struct Lane {
     // bitwise conditions throughout the per-instruction path: each is a
     // select, never a branch
     const bool bootw = (boot_en != 0u) & (x < 0x100u);
-    const uint32_t roff = bootw ? rom_len + x : (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
-    const uint32_t coff = ram_ok ? ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane : lane;
+    const uint32_t win = (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
+    const uint32_t roff = win + ((rom_len + x - win) & (0u - (uint32_t)bootw));
+    const uint32_t coff = (mbc == MBC_ROM_ONLY || !ram_ok) ? lane
+                          : ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane;
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
     p = cart ? cramb + coff : p;
     p = rom ? this->rom + roff : p;
