@@ -670,11 +670,20 @@ struct Lane {
   // up to the nearest of those, the last one ending at or before it.
   __device__ int poll_passes(uint32_t dw, uint32_t ly, int cframe) const {
     const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
-    const bool z = ly == d8, c = ly < d8;
-    const bool back = cc == 0u ? !z : cc == 1u ? z : cc == 2u ? !c : c;
-    if (!back || ime_delay != 0u || (ime != 0u && (ie & ifr & 0x1Fu) != 0u)) return 0;
+    // cc: 0 NZ, 1 Z, 2 NC, 3 C
+    const bool flag = (cc & 2u) ? ly < d8 : ly == d8;
+    const bool back = flag == ((cc & 1u) != 0u);
+    if ((!back) | (ime_delay != 0u) | ((ime != 0u) & ((ie & ifr & 0x1Fu) != 0u))) return 0;
     int d = kCyclesPerFrame - cframe;
-    if (lcdc & 0x80u) d = min(d, kCyclesPerLine - (int)scan);
+    if (lcdc & 0x80u) {
+      // A scanline change compares the new line's STAT bits with those at
+      // the start of the step that crosses it.  With the HBlank source
+      // enabled that step must start in mode 0 as the reference's last
+      // instruction of the line does, so passes stop at mode boundaries too.
+      const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
+      const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
+      d = min(d, nb - (int)scan);
+    }
     if (pend) {
       d = min(d, max((int)delay, 1));
     } else if (tac & 4u) {

@@ -2,9 +2,10 @@
 
 The step kernel advances whole passes of such a loop in one step up to the
 next scanline, TIMA overflow, frame end or interrupt service.  These carts
-poll with every jump condition while timer, STAT (LYC) and VBlank interrupts
-fire with IME on or off, the LCD is switched off and on, and TIMA runs at
-every rate; state is compared in full after every step.
+poll with every jump condition while timer, VBlank and STAT interrupts (LYC,
+HBlank and VBlank sources) fire with IME on or off, the LCD is switched off
+and on, and TIMA runs at every rate; state is compared in full after every
+step.
 """
 
 from __future__ import annotations
@@ -22,7 +23,7 @@ from .conftest import require_gpu
 pytestmark = pytest.mark.gpu
 
 
-def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool) -> bytes:
+def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, stat: int = 0x40) -> bytes:
     """A 32 KiB ROM-only cart whose main loop waits on LY four ways."""
     rng = np.random.default_rng(seed)
     rom = bytearray(0x8000)
@@ -56,8 +57,8 @@ def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool) -> 
     a.ldh_a8_a(0x07)  # TAC
     a.ld_r_d8("A", int(rng.integers(0, 154)))
     a.ldh_a8_a(0x45)  # LYC
-    a.ld_r_d8("A", 0x40)
-    a.ldh_a8_a(0x41)  # STAT: LYC interrupt source
+    a.ld_r_d8("A", stat)
+    a.ldh_a8_a(0x41)  # STAT interrupt sources
     a.ld_r_d8("A", ie)
     a.ldh_a8_a(0xFF)
     a.ld_r_d8("A", 0x00)
@@ -103,21 +104,24 @@ def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool) -> 
 
 
 CASES = [
-    # seed, IME, IE, TAC, LCD-off frames
-    (1, True, 0x07, 0x05, False),
-    (2, True, 0x05, 0x04, False),
-    (3, False, 0x07, 0x07, False),
-    (4, True, 0x03, 0x00, True),
-    (5, True, 0x04, 0x06, True),
+    # seed, IME, IE, TAC, LCD-off frames, STAT sources (LYC 0x40, HBlank 0x08, VBlank 0x10)
+    (1, True, 0x07, 0x05, False, 0x40),
+    (2, True, 0x05, 0x04, False, 0x40),
+    (3, False, 0x07, 0x07, False, 0x40),
+    (4, True, 0x03, 0x00, True, 0x40),
+    (5, True, 0x04, 0x06, True, 0x40),
+    (6, True, 0x02, 0x00, False, 0x08),
+    (7, True, 0x03, 0x05, False, 0x58),
+    (8, False, 0x02, 0x00, True, 0x18),
 ]
 
 
-@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off", CASES)
-def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off):
+@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off,stat", CASES)
+def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
 
-    rom = poll_cart(seed, ime, ie, tac, lcd_off)
+    rom = poll_cart(seed, ime, ie, tac, lcd_off, stat)
     n, fs, steps = 64, 24, 4
     dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
                         stage="emulate_only", bootrom=bootstub)  # fmt: skip
@@ -135,6 +139,8 @@ def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off):
         assert int(mem[0, 0xC000]) > 0  # the loops completed passes
         if ime and ie & 4 and tac & 4:
             assert int(mem[0, 0xDF02]) > 0  # timer interrupts were serviced
+        if ime and ie & 2 and stat & 0x08:
+            assert int(mem[0, 0xDF01]) > 0  # HBlank STAT interrupts were serviced
         assert int(ref.field("trap_flag").sum()) == 0
     finally:
         dut.close()
