@@ -656,9 +656,10 @@ struct Lane {
 
   // Cycles a halted CPU advances in one loop iteration: the reference steps
   // 4 cycles at a time and checks IE & IF after each; nothing it can observe
-  // changes before the next PPU mode or line boundary, the next timer
-  // overflow or reload, or the end of the frame, so it advances straight to
-  // the first 4-cycle step that reaches the nearest of those.  A request
+  // changes before the next line boundary (and, with the HBlank STAT source
+  // on, the next mode boundary), the next timer overflow or reload, or the
+  // end of the frame, so it advances straight to the first 4-cycle step that
+  // reaches the nearest of those.  A request
   // already pending (a launch that ended before its interrupt check, or
   // imported state) wakes the CPU after the first 4 cycles.
   // Whole passes of an LY poll loop (LDH A,(44); CP d8; JR cc,back; 32
@@ -697,10 +698,10 @@ struct Lane {
     if (ie & ifr & 0x1Fu) return 4;
     int d = kCyclesPerFrame - cframe;
     if (lcdc & 0x80u) {
-      const int nb = ly >= (uint32_t)kScreenH ? kCyclesPerLine
-                     : scan < 80u             ? 80
-                     : scan < 250u            ? 250
-                                              : kCyclesPerLine;
+      // with the HBlank STAT source on, the step that crosses into the next
+      // line must start in mode 0 as the reference's last 4-cycle step does
+      const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
+      const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
       d = min(d, nb - (int)scan);
     }
     if (pend) {

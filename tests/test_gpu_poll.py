@@ -23,8 +23,10 @@ from .conftest import require_gpu
 pytestmark = pytest.mark.gpu
 
 
-def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, stat: int = 0x40) -> bytes:
-    """A 32 KiB ROM-only cart whose main loop waits on LY four ways."""
+def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, stat: int = 0x40,
+              halt: bool = False) -> bytes:
+    """A 32 KiB ROM-only cart whose main loop waits on LY four ways (and, with
+    ``halt``, in HALT until an interrupt request)."""
     rng = np.random.default_rng(seed)
     rom = bytearray(0x8000)
     h = Asm(origin=0x0068)
@@ -85,6 +87,9 @@ def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, sta
     a.ldh_a_a8(0x44)
     a.alu_d8("CP", lines[1])
     a.jr("w4", "NC")
+    if halt:
+        a.halt()
+        a.nop()  # an IME=0 wake skips this byte
     a.ld_a_a16(0xC000)
     a.inc_r("A")
     a.ld_a16_a(0xC000)
@@ -114,14 +119,23 @@ CASES = [
     (7, True, 0x03, 0x05, False, 0x58),
     (8, False, 0x02, 0x00, True, 0x18),
 ]
+# HALT waits between the polls (the halted CPU's fast-forward follows the
+# same event rule)
+HALT_CASES = [
+    (9, True, 0x02, 0x00, False, 0x08),
+    (10, True, 0x07, 0x05, False, 0x48),
+    (11, False, 0x06, 0x04, False, 0x08),
+    (12, True, 0x01, 0x06, True, 0x10),
+]
 
 
-@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off,stat", CASES)
-def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat):
+@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off,stat,halt",
+                         [c + (False,) for c in CASES] + [c + (True,) for c in HALT_CASES])  # fmt: skip
+def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat, halt):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
 
-    rom = poll_cart(seed, ime, ie, tac, lcd_off, stat)
+    rom = poll_cart(seed, ime, ie, tac, lcd_off, stat, halt)
     n, fs, steps = 64, 24, 4
     dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
                         stage="emulate_only", bootrom=bootstub)  # fmt: skip
