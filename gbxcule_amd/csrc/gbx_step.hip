@@ -318,9 +318,21 @@ struct Lane {
   __device__ void timer_tick(int cycles) {
     if (cycles <= 0) return;
     uint32_t d = div & 0xFFFFu;
+    bool done = false;
     if ((pend == 0u) & ((d & tmask) + (uint32_t)cycles <= tmask)) {
       d = (d + (uint32_t)cycles) & 0xFFFFu;  // no edge, no reload: DIV only
-    } else {
+      done = true;
+    } else if (pend == 0u) {
+      // n falling edges of the selected DIV bit and no overflow: TIMA += n
+      const uint32_t n = ((d & tmask) + (uint32_t)cycles) >> (div_bit(tac) + 1u);
+      if (tima + n <= 0xFFu) {
+        tima += n;
+        d = (d + (uint32_t)cycles) & 0xFFFFu;
+        M(0xFF05) = tima;
+        done = true;
+      }
+    }
+    if (!done) {
       int rem = cycles;
       while (rem > 0) {
         if (pend && (int)delay <= 0) reload_now();
