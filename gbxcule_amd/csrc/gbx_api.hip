@@ -84,9 +84,11 @@ std::vector<Rec> build_records(const uint8_t* rom, int64_t rom_bytes, const uint
     }
   };
   fill(rom, rom_bytes, 0);
-  // LY poll loops whose six bytes lie inside one 16 KiB window
-  for (int64_t i = 0; i + 5 < rom_bytes; ++i)
+  // LY poll loops and block-copy loops whose bytes lie inside one 16 KiB window
+  for (int64_t i = 0; i + 5 < rom_bytes; ++i) {
     if ((i & 0x3FFF) <= 0x3FFA && poll_loop_at(rom + i)) r[(size_t)i] = mark_poll_loop(r[(size_t)i], rom + i);
+    if ((i & 0x3FFF) <= 0x3FF8 && i + 7 < rom_bytes && copy_loop_at(rom + i)) r[(size_t)i] = mark_copy_loop(r[(size_t)i]);
+  }
   fill(boot, 0x100, (size_t)rom_bytes);
   const std::vector<uint8_t> ff(kOpenBusBytes, 0xFF);
   fill(ff.data(), kOpenBusBytes, (size_t)rom_bytes + 0x100);

@@ -38,7 +38,8 @@
 // w9  SW1   writeback selector of W1 (F always takes the new flags)
 // w10 FL    [0:7] flags taken from the computed Z/H/C  [8:15] flags not forced to 0
 //           [16:23] flags inverted last  [24] IME write  [25] IME value  [26] HALT
-//           [27] trap  [28] LY poll loop starts here (set by the record builder)
+//           [27] trap  [28] LY poll or block-copy loop starts here (set by the
+//           record builder)
 //           [29] SP takes the 16-bit sum  [30] DAA
 // w11 TN    not taken [0:4] cycles [5:6] bus writes [7:9] SP delta (signed);
 //           taken the same at [16:25]
@@ -50,7 +51,8 @@
 //           result mask (0xFF)
 // w15 DW    bus write addresses: operand address + DW, per 16-bit half (wrapping);
 //           for a poll-loop start (FL bit 28, a read): [0:7] the CP constant,
-//           [8:9] the JR condition (0 NZ, 1 Z, 2 NC, 3 C)
+//           [8:9] the JR condition (0 NZ, 1 Z, 2 NC, 3 C); for a block-copy
+//           loop start: [31] set
 #pragma once
 #include <stdint.h>
 
@@ -459,6 +461,22 @@ __host__ __device__ constexpr bool poll_loop_at(const uint8_t* p) {
 __host__ __device__ constexpr Rec mark_poll_loop(Rec r, const uint8_t* p) {
   r.w[10] |= kPollFlag;
   r.w[15] = p[3] | (((uint32_t)(p[4] - 0x20u) >> 3) << 8);
+  return r;
+}
+// The block-copy loop LD A,(HL+); LD (DE),A; INC DE; DEC BC; LD A,B; OR C
+// (or LD A,C; OR B); JR NZ back to the LD (displacement -8): its LD A,(HL+)
+// carries the same FL bit, and
+// bit 31 of its last word (free: the LD writes nothing) tells it from a poll
+// loop.
+constexpr uint32_t kCopyLoop = 1u << 31;
+__host__ __device__ constexpr bool copy_loop_at(const uint8_t* p) {
+  return p[0] == 0x2Au && p[1] == 0x12u && p[2] == 0x13u && p[3] == 0x0Bu &&
+         ((p[4] == 0x78u && p[5] == 0xB1u) || (p[4] == 0x79u && p[5] == 0xB0u)) && p[6] == 0x20u &&
+         p[7] == 0xF8u;
+}
+__host__ __device__ constexpr Rec mark_copy_loop(Rec r) {
+  r.w[10] |= kPollFlag;
+  r.w[15] = kCopyLoop;
   return r;
 }
 

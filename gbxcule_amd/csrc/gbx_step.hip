@@ -681,18 +681,15 @@ struct Lane {
   // count after each; nothing it observes changes before the next scanline
   // (LY), TIMA overflow, frame end or interrupt service, so passes are taken
   // up to the nearest of those, the last one ending at or before it.
-  __device__ int poll_passes(uint32_t dw, uint32_t ly, int cframe) const {
-    const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
-    // cc: 0 NZ, 1 Z, 2 NC, 3 C
-    const bool flag = (cc & 2u) ? ly < d8 : ly == d8;
-    const bool back = flag == ((cc & 1u) != 0u);
-    if ((!back) | (ime_delay != 0u) | ((ime != 0u) & ((ie & ifr & 0x1Fu) != 0u))) return 0;
+  // Cycles from here to the nearest event that a batched step must not pass:
+  // the frame end, the scanline end, a TIMA overflow or reload.  A scanline
+  // change compares the new line's STAT bits with those at the start of the
+  // step that crosses it.  With the HBlank source enabled that step must
+  // start in mode 0 as the reference's last instruction of the line does,
+  // so the mode boundaries count as well.
+  __device__ int ff_horizon(int cframe) const {
     int d = kCyclesPerFrame - cframe;
     if (lcdc & 0x80u) {
-      // A scanline change compares the new line's STAT bits with those at
-      // the start of the step that crosses it.  With the HBlank source
-      // enabled that step must start in mode 0 as the reference's last
-      // instruction of the line does, so passes stop at mode boundaries too.
       const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
       const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
       d = min(d, nb - (int)scan);
@@ -704,7 +701,58 @@ struct Lane {
       const int edge = period - (int)(div & (uint32_t)(period - 1));
       d = min(d, edge + (int)(255u - tima) * period);
     }
-    return d >= 32 ? d / 32 : 0;
+    return d;
+  }
+  // No pass may be batched while an interrupt would be serviced after the
+  // current instruction or the EI delay is pending.
+  __device__ bool ff_blocked() const {
+    return (ime_delay != 0u) | ((ime != 0u) & ((ie & ifr & 0x1Fu) != 0u));
+  }
+  __device__ int poll_passes(uint32_t dw, uint32_t ly, int cframe) const {
+    const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
+    // cc: 0 NZ, 1 Z, 2 NC, 3 C
+    const bool flag = (cc & 2u) ? ly < d8 : ly == d8;
+    const bool back = flag == ((cc & 1u) != 0u);
+    if ((!back) | ff_blocked()) return 0;
+    return ff_horizon(cframe) / 32;
+  }
+  // End of the plain RAM window holding x (video RAM, work RAM), else 0.
+  __device__ static uint32_t ram_window_end(uint32_t x) {
+    return x - 0x8000u < 0x2000u ? 0xA000u : x - 0xC000u < 0x2000u ? 0xE000u : 0u;
+  }
+  // Whole passes of a block-copy loop (52 cycles, 7 instructions each) that
+  // all jump back and can run as one step: bounded by the event horizon, by
+  // BC, and by the source and destination staying inside one window each
+  // (a ROM bank window above the boot image, video RAM or work RAM for the
+  // source; video or work RAM for the destination) where every byte is a
+  // plain load or store.  A destination ahead of an overlapping source stops
+  // before the first byte a pass would read after an earlier pass wrote it.
+  __device__ int copy_passes(uint32_t hl, uint32_t de, uint32_t bc, int cframe) const {
+    if (ff_blocked()) return 0;
+    const uint32_t se = hl < 0x4000u ? (((boot_en != 0u) & (hl < 0x100u)) ? 0u : 0x4000u)
+                        : hl < 0x8000u ? 0x8000u : ram_window_end(hl);
+    const uint32_t de_end = ram_window_end(de);
+    if ((se == 0u) | (de_end == 0u)) return 0;
+    int k = ff_horizon(cframe) / 52;
+    k = min(k, (int)((bc - 1u) & 0xFFFFu));  // BC = 0 runs 65536 passes
+    k = min(k, (int)(se - hl));
+    k = min(k, (int)(de_end - de));
+    if ((hl >= 0x8000u) & (de > hl)) k = min(k, (int)(de - hl));
+    return k;
+  }
+  // The memory effect of k passes: bytes src..src+k-1 to dst..dst+k-1, in
+  // batches of eight loads then eight stores (windows as copy_passes checks).
+  __device__ void block_copy(uint32_t src, uint32_t dst, int k) {
+    const uint8_t* ps = bus_ptr(src);
+    const uint32_t ss = src < 0x8000u ? 1u : (uint32_t)kEnvBlock;
+    for (int j = 0; j < k; j += 8) {
+      uint32_t v[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = (j + t < k) ? (uint32_t)ld_global(ps + (uint32_t)(j + t) * ss) : 0u;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (j + t < k) M(dst + (uint32_t)(j + t)) = v[t];
+    }
   }
   __device__ int halt_cycles(int cframe) const {
     if (ie & ifr & 0x1Fu) return 4;
@@ -942,7 +990,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           trap_op = (int)op;
           trap_kind = 1;
         }
-        if (!dbg && (o.misc & 16u)) {
+        if (!dbg && (o.misc & 16u) && (rec.w[15] & kCopyLoop)) {
+          // LD A,(HL+) of a block-copy loop just ran: advance k whole passes
+          // (this LD included) in one step.  Each pass copies (HL+) to (DE)
+          // and steps DE and BC; OR leaves Z clear (BC stays non-zero), N,
+          // H and C clear, so F = 0 and A = B | C.
+          const uint32_t hl = in.w1 >> 16, de = in.w0 & 0xFFFFu, bc = in.w0 >> 16;
+          const int k = L.copy_passes(hl, de, bc, cframe);
+          if (k > 0) {
+            L.block_copy(hl, de, k);
+            const uint32_t nbc = (bc - (uint32_t)k) & 0xFFFFu;
+            L.w0 = (nbc << 16) | (de + (uint32_t)k);
+            L.w1 = ((hl + (uint32_t)k) << 16) | ((nbc | (nbc >> 8)) & 0xFFu);
+            npc = pc;
+            cycles = 52 * k;
+            ninstr += 7u * (uint32_t)k - 1u;
+          }
+        } else if (!dbg && (o.misc & 16u)) {
           // LDH A,(44) just read LY into A; if CP d8 / JR cc takes the jump
           // back, every pass until LY or anything else can change reads the
           // same LY and leaves the same A and F: advance k whole passes (this

@@ -85,4 +85,15 @@ void harness_poll(const uint8_t* p, uint32_t* out) {
   out[2] = r.w[15];
 }
 
+// out: [is a block-copy loop start, FL word, DW word] of the decoded and
+// marked record at p (8 bytes)
+void harness_copy(const uint8_t* p, uint32_t* out) {
+  gbx::Rec r = gbx::decode_insn(p[0], p[1], p[2]);
+  const bool copy = gbx::copy_loop_at(p);
+  if (copy) r = gbx::mark_copy_loop(r);
+  out[0] = copy ? 1u : 0u;
+  out[1] = r.w[10];
+  out[2] = r.w[15];
+}
+
 }  // extern "C"

@@ -45,6 +45,7 @@ def harness(tmp_path_factory):
     lib.harness_decode.argtypes = [ctypes.c_uint32] * 3 + [u32p]
     lib.harness_exec.argtypes = [u32p, u32p]
     lib.harness_poll.argtypes = [ctypes.c_char_p, u32p]
+    lib.harness_copy.argtypes = [ctypes.c_char_p, u32p]
     return lib
 
 
@@ -218,3 +219,44 @@ def test_poll_loop_marking(harness):
     ):
         harness.harness_poll(bytes(bad), out)
         assert out[0] == 0 and not out[1] & (1 << 28)
+
+
+def test_copy_loop_marking(harness):
+    """The record builder marks exactly LD A,(HL+); LD (DE),A; INC DE; DEC BC;
+    LD A,B; OR C (or LD A,C; OR B); JR NZ back to the LD (displacement -8),
+    and the marked LD A,(HL+)
+    still decodes as itself (one read, no writes, 8 cycles)."""
+    out = _arr(3)
+    plain = _arr(16)
+    harness.harness_decode(0x2A, 0x12, 0x13, plain)
+    for tail in ([0x78, 0xB1], [0x79, 0xB0]):
+        harness.harness_copy(bytes([0x2A, 0x12, 0x13, 0x0B] + tail + [0x20, 0xF8]), out)
+        assert out[0] == 1 and out[1] == plain[10] | (1 << 28) and out[2] == 1 << 31
+        assert plain[15] == 0 and (plain[7] >> 8) & 3 == 1 and (plain[11] >> 5) & 3 == 0
+    for bad in (
+        [0x2A, 0x12, 0x13, 0x0B, 0x78, 0xB1, 0x20, 0xF9],  # jumps into the loop
+        [0x2A, 0x12, 0x13, 0x0B, 0x78, 0xB1, 0x28, 0xF8],  # JR Z
+        [0x2A, 0x12, 0x13, 0x0B, 0x78, 0xB0, 0x20, 0xF8],  # LD A,B; OR B
+        [0x3A, 0x12, 0x13, 0x0B, 0x78, 0xB1, 0x20, 0xF8],  # LD A,(HL-)
+        [0x2A, 0x12, 0x1B, 0x0B, 0x78, 0xB1, 0x20, 0xF8],  # DEC DE
+        [0x2A, 0x22, 0x13, 0x0B, 0x78, 0xB1, 0x20, 0xF8],  # LD (HL+),A
+    ):
+        harness.harness_copy(bytes(bad), out)
+        assert out[0] == 0 and not out[1] & (1 << 28)
+
+
+def test_copy_loops_in_carts_are_marked(harness):
+    """Every copy loop of the C3 cart and of the copy-loop parity carts
+    matches the marked pattern, so those tests run the batched passes."""
+    from gbxcule_amd.carts.synth import cart_c3
+    from tests.test_gpu_copy import CASES, copy_cart
+
+    out = _arr(3)
+
+    def marked(rom: bytes) -> int:
+        return sum(1 for i in range(len(rom) - 8) if rom[i] == 0x2A and
+                   (harness.harness_copy(rom[i : i + 8], out), out[0])[1] == 1)  # fmt: skip
+
+    assert marked(cart_c3(2)) == 4
+    for case in CASES:
+        assert marked(copy_cart(*case)) == (13 if case[5] else 12)
