@@ -682,14 +682,14 @@ struct Lane {
   // (LY), TIMA overflow, frame end or interrupt service, so passes are taken
   // up to the nearest of those, the last one ending at or before it.
   // Cycles from here to the nearest event that a batched step must not pass:
-  // the frame end, the scanline end, a TIMA overflow or reload.  A scanline
-  // change compares the new line's STAT bits with those at the start of the
-  // step that crosses it.  With the HBlank source enabled that step must
-  // start in mode 0 as the reference's last instruction of the line does,
-  // so the mode boundaries count as well.
-  __device__ int ff_horizon(int cframe) const {
+  // the frame end, a TIMA overflow or reload, and with `lines` the scanline
+  // end.  A scanline change compares the new line's STAT bits with those at
+  // the start of the step that crosses it.  With the HBlank source enabled
+  // that step must start in mode 0 as the reference's last instruction of
+  // the line does, so the mode boundaries count as well.
+  __device__ int ff_horizon(int cframe, bool lines) const {
     int d = kCyclesPerFrame - cframe;
-    if (lcdc & 0x80u) {
+    if ((lcdc & 0x80u) && lines) {
       const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
       const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
       d = min(d, nb - (int)scan);
@@ -714,7 +714,7 @@ struct Lane {
     const bool flag = (cc & 2u) ? ly < d8 : ly == d8;
     const bool back = flag == ((cc & 1u) != 0u);
     if ((!back) | ff_blocked()) return 0;
-    return ff_horizon(cframe) / 32;
+    return ff_horizon(cframe, true) / 32;
   }
   // End of the plain RAM window holding x (video RAM, work RAM), else 0.
   __device__ static uint32_t ram_window_end(uint32_t x) {
@@ -727,13 +727,21 @@ struct Lane {
   // source; video or work RAM for the destination) where every byte is a
   // plain load or store.  A destination ahead of an overlapping source stops
   // before the first byte a pass would read after an earlier pass wrote it.
+  // The loop reads no IO, so scanline changes bound the passes only when
+  // the HBlank STAT source is on (see ff_horizon) or when a VBlank or STAT
+  // request could be serviced; otherwise one step runs through several
+  // lines, whose changes the PPU step applies in order exactly as the
+  // reference's per-instruction steps do: the STAT bits each change compares
+  // against are those of the change before it (mode 0 or 1 and the same
+  // coincidence as at the end of the line's last instruction).
   __device__ int copy_passes(uint32_t hl, uint32_t de, uint32_t bc, int cframe) const {
     if (ff_blocked()) return 0;
+    const bool lines = ((stat_full & 0x08u) != 0u) | ((ime != 0u) & ((ie & 0x03u) != 0u));
     const uint32_t se = hl < 0x4000u ? (((boot_en != 0u) & (hl < 0x100u)) ? 0u : 0x4000u)
                         : hl < 0x8000u ? 0x8000u : ram_window_end(hl);
     const uint32_t de_end = ram_window_end(de);
     if ((se == 0u) | (de_end == 0u)) return 0;
-    int k = ff_horizon(cframe) / 52;
+    int k = ff_horizon(cframe, lines) / 52;
     k = min(k, (int)((bc - 1u) & 0xFFFFu));  // BC = 0 runs 65536 passes
     k = min(k, (int)(se - hl));
     k = min(k, (int)(de_end - de));
