@@ -666,33 +666,38 @@ struct Lane {
     return lc;
   }
 
-  // Cycles a halted CPU advances in one loop iteration: the reference steps
-  // 4 cycles at a time and checks IE & IF after each; nothing it can observe
-  // changes before the next line boundary (and, with the HBlank STAT source
-  // on, the next mode boundary), the next timer overflow or reload, or the
-  // end of the frame, so it advances straight to the first 4-cycle step that
-  // reaches the nearest of those.  A request
-  // already pending (a launch that ended before its interrupt check, or
-  // imported state) wakes the CPU after the first 4 cycles.
-  // Whole passes of an LY poll loop (LDH A,(44); CP d8; JR cc,back; 32
-  // cycles) that can be taken in one step from the LDH that just read ly:
-  // 0 unless the jump back is taken.  The reference runs the loop one
-  // instruction at a time with the timer, PPU, interrupt check and frame
-  // count after each; nothing it observes changes before the next scanline
-  // (LY), TIMA overflow, frame end or interrupt service, so passes are taken
-  // up to the nearest of those, the last one ending at or before it.
+  // Cycles from here to the end of the first scanline change that can raise
+  // one of the requests in `irq` (bit 0 VBlank, bit 1 STAT): the change into
+  // line 144 (VBlank, and the STAT mode-1 source) or into line LYC (the STAT
+  // LYC source).  The mode-2 source never fires at a change, and the HBlank
+  // source is handled by the caller.
+  __device__ int line_horizon(uint32_t irq) const {
+    uint32_t n = 0xFFFFu;  // changes ahead, 1 = the next one
+    if (((irq & 1u) != 0u) | (((irq & 2u) != 0u) & ((stat_full & 0x10u) != 0u)))
+      n = (144u + 153u - ly) % (uint32_t)kLinesPerFrame + 1u;
+    if (((irq & 2u) != 0u) & ((stat_full & 0x40u) != 0u) & (lyc < (uint32_t)kLinesPerFrame))
+      n = min(n, (lyc + 153u - ly) % (uint32_t)kLinesPerFrame + 1u);
+    return n == 0xFFFFu ? kCyclesPerFrame : (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(n - 1u);
+  }
   // Cycles from here to the nearest event that a batched step must not pass:
-  // the frame end, a TIMA overflow or reload, and with `lines` the scanline
-  // end.  A scanline change compares the new line's STAT bits with those at
-  // the start of the step that crosses it.  With the HBlank source enabled
-  // that step must start in mode 0 as the reference's last instruction of
-  // the line does, so the mode boundaries count as well.
-  __device__ int ff_horizon(int cframe, bool lines) const {
+  // the frame end, a TIMA overflow or reload, and scanline changes: every
+  // one with `every_line`, else those that can raise a request in `irq`
+  // (line_horizon).  The PPU step applies several changes in order exactly
+  // as the reference's per-instruction steps do, except for one thing: a
+  // change compares the new line's STAT bits with those at the start of the
+  // step that crosses it.  With the HBlank source enabled that step must
+  // start in mode 0 as the reference's last instruction of the line does, so
+  // then every change and the mode boundaries count as well.
+  __device__ int ff_horizon(int cframe, bool every_line, uint32_t irq) const {
     int d = kCyclesPerFrame - cframe;
-    if ((lcdc & 0x80u) && lines) {
-      const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
-      const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
-      d = min(d, nb - (int)scan);
+    if (lcdc & 0x80u) {
+      if (every_line | ((stat_full & 0x08u) != 0u)) {
+        const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
+        const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
+        d = min(d, nb - (int)scan);
+      } else if (irq) {
+        d = min(d, line_horizon(irq));
+      }
     }
     if (pend) {
       d = min(d, max((int)delay, 1));
@@ -708,13 +713,20 @@ struct Lane {
   __device__ bool ff_blocked() const {
     return (ime_delay != 0u) | ((ime != 0u) & ((ie & ifr & 0x1Fu) != 0u));
   }
+  // Whole passes of an LY poll loop (LDH A,(44); CP d8; JR cc,back; 32
+  // cycles) that can be taken in one step from the LDH that just read ly:
+  // 0 unless the jump back is taken.  The reference runs the loop one
+  // instruction at a time with the timer, PPU, interrupt check and frame
+  // count after each; nothing it observes changes before the next scanline
+  // (LY), TIMA overflow, frame end or interrupt service, so passes are taken
+  // up to the nearest of those, the last one ending at or before it.
   __device__ int poll_passes(uint32_t dw, uint32_t ly, int cframe) const {
     const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
     // cc: 0 NZ, 1 Z, 2 NC, 3 C
     const bool flag = (cc & 2u) ? ly < d8 : ly == d8;
     const bool back = flag == ((cc & 1u) != 0u);
     if ((!back) | ff_blocked()) return 0;
-    return ff_horizon(cframe, true) / 32;
+    return ff_horizon(cframe, true, 0u) / 32;
   }
   // End of the plain RAM window holding x (video RAM, work RAM), else 0.
   __device__ static uint32_t ram_window_end(uint32_t x) {
@@ -727,21 +739,15 @@ struct Lane {
   // source; video or work RAM for the destination) where every byte is a
   // plain load or store.  A destination ahead of an overlapping source stops
   // before the first byte a pass would read after an earlier pass wrote it.
-  // The loop reads no IO, so scanline changes bound the passes only when
-  // the HBlank STAT source is on (see ff_horizon) or when a VBlank or STAT
-  // request could be serviced; otherwise one step runs through several
-  // lines, whose changes the PPU step applies in order exactly as the
-  // reference's per-instruction steps do: the STAT bits each change compares
-  // against are those of the change before it (mode 0 or 1 and the same
-  // coincidence as at the end of the line's last instruction).
+  // The loop reads no IO, so a scanline change bounds the passes only when
+  // it can raise a VBlank or STAT request that would be serviced.
   __device__ int copy_passes(uint32_t hl, uint32_t de, uint32_t bc, int cframe) const {
     if (ff_blocked()) return 0;
-    const bool lines = ((stat_full & 0x08u) != 0u) | ((ime != 0u) & ((ie & 0x03u) != 0u));
     const uint32_t se = hl < 0x4000u ? (((boot_en != 0u) & (hl < 0x100u)) ? 0u : 0x4000u)
                         : hl < 0x8000u ? 0x8000u : ram_window_end(hl);
     const uint32_t de_end = ram_window_end(de);
     if ((se == 0u) | (de_end == 0u)) return 0;
-    int k = ff_horizon(cframe, lines) / 52;
+    int k = ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u) / 52;
     k = min(k, (int)((bc - 1u) & 0xFFFFu));  // BC = 0 runs 65536 passes
     k = min(k, (int)(se - hl));
     k = min(k, (int)(de_end - de));
@@ -762,24 +768,15 @@ struct Lane {
         if (j + t < k) M(dst + (uint32_t)(j + t)) = v[t];
     }
   }
+  // Cycles a halted CPU advances in one loop iteration: the reference steps
+  // 4 cycles at a time and wakes on IE & IF; nothing it can observe changes
+  // before the first event of ff_horizon for the requests IE enables, so it
+  // advances straight to the first 4-cycle step that reaches that event.  A
+  // request already pending (a launch that ended before its interrupt check,
+  // or imported state) wakes the CPU after the first 4 cycles.
   __device__ int halt_cycles(int cframe) const {
     if (ie & ifr & 0x1Fu) return 4;
-    int d = kCyclesPerFrame - cframe;
-    if (lcdc & 0x80u) {
-      // with the HBlank STAT source on, the step that crosses into the next
-      // line must start in mode 0 as the reference's last 4-cycle step does
-      const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
-      const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
-      d = min(d, nb - (int)scan);
-    }
-    if (pend) {
-      d = min(d, max((int)delay, 1));
-    } else if (tac & 4u) {
-      const int period = 1 << (div_bit(tac) + 1);
-      const int edge = period - (int)(div & (uint32_t)(period - 1));
-      d = min(d, edge + (int)(255u - tima) * period);
-    }
-    d = max(d, 1);
+    const int d = max(ff_horizon(cframe, false, ie & 0x03u), 1);
     return (d + 3) & ~3;
   }
 

@@ -119,13 +119,20 @@ CASES = [
     (7, True, 0x03, 0x05, False, 0x58),
     (8, False, 0x02, 0x00, True, 0x18),
 ]
-# HALT waits between the polls (the halted CPU's fast-forward follows the
-# same event rule)
+# HALT waits between the polls.  A halted CPU runs to the first event that
+# can wake it: with the HBlank source off, only the scanline changes into
+# line 144 (VBlank, STAT mode-1 source) and into LYC (STAT LYC source) count
+# when IE enables them; the mode-2 source never fires at a change.
 HALT_CASES = [
     (9, True, 0x02, 0x00, False, 0x08),
     (10, True, 0x07, 0x05, False, 0x48),
     (11, False, 0x06, 0x04, False, 0x08),
     (12, True, 0x01, 0x06, True, 0x10),
+    (13, True, 0x02, 0x00, False, 0x40),
+    (14, True, 0x06, 0x05, False, 0x10),
+    (15, False, 0x04, 0x07, False, 0x20),
+    (16, True, 0x03, 0x04, True, 0x40),
+    (17, True, 0x05, 0x06, False, 0x60),
 ]
 
 
