@@ -38,9 +38,13 @@ __global__ void init_state_kernel(int32_t* cs, int32_t* sc, int npad, int mbc_ki
 // ---------------------------------------------------------------------------
 // Snapshot renderer (reference kernels/ppu_render_downsampled.py:27-234).
 // One thread per (env, output row); lanes of a wavefront are consecutive envs
-// of one row, so IO/OAM/tile-map reads of the same address coalesce.  The
-// row's sprite set (first 10 OAM entries overlapping the line, counted before
-// the x test) is selected once per row instead of once per sample.
+// of one row, so IO/OAM reads of the same address coalesce.  Per row, the
+// sprites (the first 10 OAM entries overlapping the line, counted before the
+// x test) are resolved once into a line buffer of the 80 samples: each
+// sample keeps the opaque sprite pixel with the lowest x (ties: the lower
+// OAM index, the earlier entry), as the reference's per-sample search over
+// OAM selects it.  The BG/window tile row is re-read only when the sample
+// moves to another tile.
 // ---------------------------------------------------------------------------
 struct Row {
   const uint8_t* mb;  // block base
@@ -58,8 +62,16 @@ __device__ uint32_t bg_tile_addr(uint32_t lcdc, uint32_t tile_id) {
   return (uint32_t)(0x9000 + ((int)tile_id >= 128 ? (int)tile_id - 256 : (int)tile_id) * 16);
 }
 
-__global__ void render_kernel(DevState s, uint8_t* out, int64_t base, int packed) {
-  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+constexpr int kRenderThreads = 128;
+
+__global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
+                                                                int packed) {
+  // line buffer, one column per thread: 0 = no sprite pixel, else bit 15 set,
+  // [0:7] the sprite's OAM x (its left edge + 8), [8:9] colour, [10] OBP1,
+  // [11] behind non-zero BG
+  __shared__ uint16_t obj[kDsW][kRenderThreads];
+  const uint32_t t = threadIdx.x;
+  const uint32_t e = blockIdx.x * kRenderThreads + t;
   const uint32_t oy = blockIdx.y;
   if (e >= (uint32_t)s.n) return;
   Row r{s.mem + ((size_t)block_of(e) << 22), e & (kEnvBlock - 1)};
@@ -68,26 +80,52 @@ __global__ void render_kernel(DevState s, uint8_t* out, int64_t base, int packed
   const uint32_t bgp = r.M(0xFF47), obp0 = r.M(0xFF48), obp1 = r.M(0xFF49);
   const uint32_t wy = r.M(0xFF4A), wx = r.M(0xFF4B);
   const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
-  uint64_t sel = 0;
-  if (lcdc & 0x02u) {
+  const bool sprites = (lcdc & 0x02u) != 0u;
+  if (sprites) {
+    for (int ox = 0; ox < kDsW; ++ox) obj[ox][t] = 0;
     uint32_t on_line = 0;
-    for (uint32_t k = 0; k < 40u; ++k) {
+    for (uint32_t k = 0; k < 40u && on_line < 10u; ++k) {
       const uint32_t sy = r.M(0xFE00u + 4u * k), sx = r.M(0xFE01u + 4u * k);
       if (sx == 0 || sy == 0 || sx >= 168u || sy >= 160u) continue;
       const int top = (int)sy - 16;
       if ((int)y < top || (int)y >= top + (int)height) continue;
-      if (on_line >= 10u) continue;
       ++on_line;
-      sel |= 1ull << k;
+      uint32_t tile = r.M(0xFE02u + 4u * k);
+      const uint32_t attr = r.M(0xFE03u + 4u * k);
+      uint32_t row = (uint32_t)((int)y - top);
+      if ((attr >> 6) & 1u) row = height - 1u - row;
+      if (height == 16u) {
+        tile &= 0xFEu;
+        if (row >= 8u) {
+          tile += 1u;
+          row -= 8u;
+        }
+      }
+      const uint32_t ta = 0x8000u + tile * 16u + row * 2u;
+      const uint32_t lo = r.M(ta), hi = r.M(ta + 1u);
+      const uint32_t tag = 0x8000u | sx | (((attr >> 4) & 1u) << 10) | (((attr >> 7) & 1u) << 11);
+      const int left = (int)sx - 8;
+      // the sampled columns x = 2*ox inside [left, left + 8)
+      for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
+        if (x < 0 || x >= 2 * kDsW) continue;
+        const uint32_t pxl = (uint32_t)(x - left);
+        const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
+        const uint32_t color = (((hi >> bit) & 1u) << 1) | ((lo >> bit) & 1u);
+        if (color == 0) continue;
+        const uint32_t cur = obj[x >> 1][t];
+        if (cur == 0 || sx < (cur & 0xFFu)) obj[x >> 1][t] = (uint16_t)(tag | (color << 8));
+      }
     }
   }
   const bool win = (lcdc & 0x20u) && y >= wy;
+  const uint32_t bg_map = (lcdc & 0x08u) ? 0x9C00u : 0x9800u;
+  const uint32_t win_map = (lcdc & 0x40u) ? 0x9C00u : 0x9800u;
   uint32_t word = 0;
-  const int nsamp = kDsW;
+  uint32_t tkey = 0xFFFFFFFFu, tlo = 0, thi = 0;
   uint8_t* dst = out + base + (size_t)e * (packed ? (size_t)kDsWB * kDsH : (size_t)kDsW * kDsH) +
                  (size_t)oy * (packed ? kDsWB : kDsW);
   const bool aligned = (((uintptr_t)dst) & 3u) == 0;
-  for (int ox = 0; ox < nsamp; ++ox) {
+  for (int ox = 0; ox < kDsW; ++ox) {
     const uint32_t x = (uint32_t)ox * 2u;
     uint32_t shade = 0, bg_color = 0;
     if (lcdc & 0x01u) {
@@ -95,56 +133,36 @@ __global__ void render_kernel(DevState s, uint8_t* out, int64_t base, int packed
       if (win && (int)x >= (int)wx - 7) {
         px = (x - (wx - 7u)) & 0xFFu;
         py = (y - wy) & 0xFFu;
-        map = (lcdc & 0x40u) ? 0x9C00u : 0x9800u;
+        map = win_map;
       } else {
         px = (x + scx) & 0xFFu;
         py = (y + scy) & 0xFFu;
-        map = (lcdc & 0x08u) ? 0x9C00u : 0x9800u;
+        map = bg_map;
       }
-      const uint32_t tile_id = r.M(map + (py >> 3) * 32u + (px >> 3));
-      bg_color = tile_pixel(r, bg_tile_addr(lcdc, tile_id), py & 7u, 7u - (px & 7u));
+      // py is fixed within each of the two regions; the tile follows the
+      // map entry and the row within the tile
+      const uint32_t maddr = map + (py >> 3) * 32u + (px >> 3);
+      const uint32_t key = maddr | ((py & 7u) << 16);
+      if (key != tkey) {
+        const uint32_t ta = bg_tile_addr(lcdc, r.M(maddr)) + (py & 7u) * 2u;
+        tlo = r.M(ta);
+        thi = r.M(ta + 1u);
+        tkey = key;
+      }
+      const uint32_t bit = 7u - (px & 7u);
+      bg_color = (((thi >> bit) & 1u) << 1) | ((tlo >> bit) & 1u);
       shade = (bgp >> (bg_color * 2u)) & 3u;
     }
-    if (sel) {
-      bool found = false;
-      int best_x = 0;
-      uint32_t best_color = 0, best_attr = 0;
-      // OAM order: ties on x keep the lower index, as the reference does
-      for (uint64_t m = sel; m; m &= m - 1) {
-        const uint32_t k = (uint32_t)__builtin_ctzll(m);
-        const int left = (int)r.M(0xFE01u + 4u * k) - 8;
-        if ((int)x < left || (int)x >= left + 8) continue;
-        const int top = (int)r.M(0xFE00u + 4u * k) - 16;
-        uint32_t tile = r.M(0xFE02u + 4u * k);
-        const uint32_t attr = r.M(0xFE03u + 4u * k);
-        uint32_t row = (uint32_t)((int)y - top);
-        if ((attr >> 6) & 1u) row = height - 1u - row;
-        if (height == 16u) {
-          tile &= 0xFEu;
-          if (row >= 8u) {
-            tile += 1u;
-            row -= 8u;
-          }
-        }
-        const uint32_t pxl = (uint32_t)((int)x - left);
-        const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
-        const uint32_t color = tile_pixel(r, 0x8000u + tile * 16u, row, bit);
-        if (color == 0) continue;
-        if (!found || left < best_x) {
-          found = true;
-          best_x = left;
-          best_color = color;
-          best_attr = attr;
-        }
-      }
-      if (found && !(((best_attr >> 7) & 1u) && bg_color != 0)) {
-        const uint32_t pal = ((best_attr >> 4) & 1u) ? obp1 : obp0;
-        shade = (pal >> (best_color * 2u)) & 3u;
+    if (sprites) {
+      const uint32_t o = obj[ox][t];
+      if (o != 0u && !(((o >> 11) & 1u) && bg_color != 0)) {
+        const uint32_t pal = ((o >> 10) & 1u) ? obp1 : obp0;
+        shade = (pal >> (((o >> 8) & 3u) * 2u)) & 3u;
       }
     }
     if (packed) {
       word |= shade << (2u * (ox & 3) + 8u * ((ox >> 2) & 3));
-      if ((ox & 15) == 15 || ox == nsamp - 1) {
+      if ((ox & 15) == 15 || ox == kDsW - 1) {
         const int b0 = (ox >> 2) & ~3;  // first byte of this word
         const int nb = (ox >> 2) - b0 + 1;
         if (aligned && nb == 4) {
@@ -278,23 +296,28 @@ __global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int wi
   if (i < 2u) snap.cnt[i] = s.cnt[cnt_index(env, (int)i)];
 }
 
-// Masked restore of the interleaved images (mem + cart RAM).  Thread = (env,
-// chunk of addresses); unmasked lanes leave at once, so wavefronts with no
-// masked env cost nothing beyond their launch.
-constexpr uint32_t kResetChunk = 1024;
-__global__ void masked_mem_kernel(DevState s, const uint8_t* snap_mem, const uint8_t* snap_cram,
-                                  const uint8_t* mask) {
-  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (uint32_t)s.n || !mask[e]) return;
-  const uint32_t chunk = blockIdx.y;
+// Masked restore of the interleaved images (mem + cart RAM).  One wavefront
+// per (64-env block, chunk of address rows): the lanes run over the chunk's
+// rows, each reads the row's snapshot byte once, and one store per masked
+// env of the block writes that env's byte in 64 rows.  Blocks without a
+// masked env leave at once.
+constexpr uint32_t kResetRows = 4096;
+__global__ __launch_bounds__(kEnvBlock) void masked_mem_kernel(DevState s, const uint8_t* snap_mem,
+                                                               const uint8_t* snap_cram,
+                                                               const uint8_t* mask) {
+  const uint32_t b = blockIdx.x, l = threadIdx.x;
+  const uint32_t e = (b << kEnvBlockShift) | l;
+  const uint64_t bits = __ballot(e < (uint32_t)s.n && mask[e] != 0);
+  if (bits == 0) return;
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t a0 = chunk * kResetChunk;
-  for (uint32_t a = a0; a < a0 + kResetChunk && a < per_env; ++a) {
-    if (a < (uint32_t)kMemSize) s.mem[mem_index(e, a)] = snap_mem[a];
-    else {
-      const uint32_t off = a - (uint32_t)kMemSize;
-      s.cram[cram_index(e, off, (uint32_t)s.cram_stride)] = snap_cram[off];
-    }
+  const uint32_t a1 = min(per_env, (blockIdx.y + 1u) * kResetRows);
+  for (uint32_t a = blockIdx.y * kResetRows + l; a < a1; a += kEnvBlock) {
+    const bool in_mem = a < (uint32_t)kMemSize;
+    const uint32_t off = a - (uint32_t)kMemSize;
+    const uint8_t v = in_mem ? snap_mem[a] : snap_cram[off];
+    uint8_t* row = in_mem ? s.mem + mem_index(b << kEnvBlockShift, a)
+                          : s.cram + cram_index(b << kEnvBlockShift, off, (uint32_t)s.cram_stride);
+    for (uint64_t q = bits; q; q &= q - 1) row[__builtin_ctzll(q)] = v;
   }
 }
 
@@ -436,8 +459,8 @@ hipError_t launch_render_bg_env0(const DevState& s, uint8_t* out, hipStream_t st
 hipError_t launch_render(const DevState& s, uint8_t* out, int64_t base, int packed,
                          hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(render_kernel, dim3((unsigned)((s.n + 255) / 256), kDsH), dim3(256), 0, st, s,
-                     out, base, packed);
+  hipLaunchKernelGGL(render_kernel, dim3((unsigned)((s.n + kRenderThreads - 1) / kRenderThreads), kDsH),
+                     dim3(kRenderThreads), 0, st, s, out, base, packed);
   return hipGetLastError();
 }
 
@@ -452,9 +475,9 @@ hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const u
                                hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t chunks = (per_env + kResetChunk - 1) / kResetChunk;
-  hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + 255) / 256), chunks), dim3(256), 0,
-                     st, s, snap.mem, snap.cram, mask);
+  const uint32_t chunks = (per_env + kResetRows - 1) / kResetRows;
+  hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + kEnvBlock - 1) / kEnvBlock), chunks),
+                     dim3(kEnvBlock), 0, st, s, snap.mem, snap.cram, mask);
   hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)s.n), dim3(256), 0, st, s, snap, mask,
                      snap.has_pix);
   return hipGetLastError();

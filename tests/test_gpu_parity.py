@@ -85,16 +85,18 @@ def test_step_parity(carts, bootstub, cart, n, fs, steps, seed, render):
         ref.close()
 
 
-def test_masked_reset_and_senses_parity(carts, bootstub):
+@pytest.mark.parametrize("cart,n", [("c5", 128), ("c4m3", 200)])
+def test_masked_reset_and_senses_parity(carts, bootstub, cart, n):
     """C5 shape in miniature: snapshot at step 0, ~10% masked restores per
-    step, unpacked pixels and a 32-byte RAM-sense gather every step."""
+    step, unpacked pixels and a 32-byte RAM-sense gather every step (the
+    MBC3 cart also restores its 32 KiB of cart RAM per env)."""
     require_gpu()
     import torch
 
     from gbxcule_amd.reset_cache import ResetCache
 
-    rom = carts["c5"]
-    n, fs = 128, 24
+    rom = carts[cart]
+    fs = 24
     dut = _backend(rom, bootstub, n, fs, "unpacked")
     ref = RefMachine(n, rom, bootstub)
     rng = np.random.default_rng(5)
