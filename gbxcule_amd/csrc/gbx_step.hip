@@ -558,7 +558,8 @@ struct Lane {
   }
   __device__ void write8(uint32_t addr, uint32_t v) {
     const uint32_t x = fold(addr);
-    if (!write_is_special(x)) M(x) = v;
+    // FF00 stores the joypad read for the written select bits (io_write)
+    if (!write_is_special(x) & (x != 0xFF00u)) M(x) = v;
     else write_special(x, v);
   }
   // The instruction's bus writes, in order (n = 0, 1 or 2).  When none is

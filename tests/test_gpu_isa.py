@@ -134,3 +134,68 @@ def test_every_opcode_from_random_states(bootstub, cart):
     finally:
         dut.close()
         ref.close()
+
+
+# stack pointers and LD (a16),SP targets whose two written bytes straddle
+# FF00 (JOYP), IE, IO registers with side effects, MBC registers, cart RAM,
+# echo RAM, OAM and HRAM
+EDGE_SP = [0xFF01, 0xFF02, 0x0001, 0x0000, 0xA001, 0xFF81, 0xE001, 0xFEA1, 0xFF10, 0x8001,
+           0xC001, 0xFF06, 0xFF46, 0xFF51, 0x2001, 0x4001]  # fmt: skip
+EDGE_A16 = [0xFEFF, 0xFFFF, 0xFF00, 0x7FFF, 0x9FFF, 0xBFFF, 0xDFFF, 0xFF0E, 0xFF45, 0xFF04,
+            0x1FFF, 0x3FFF, 0x5FFF, 0xFDFF, 0xFF7F]  # fmt: skip
+
+
+@pytest.mark.parametrize("cart", CARTS, ids=["rom_only", "mbc1", "mbc3_ram"])
+def test_two_byte_writes_at_region_edges(bootstub, cart):
+    """PUSH, CALL, RST and LD (a16),SP whose two bytes land on two different
+    kinds of address (one of them often FF00, whose stored value is the
+    joypad read for the written select bits)."""
+    require_gpu()
+    from gbxcule_amd.backend import HipVecBackend
+    from oracle.ref import RefMachine
+
+    from ._isa import flat_rom
+
+    rng = np.random.default_rng(77 + cart[0])
+    size = (32 * 1024) << cart[1]
+    body = rng.integers(0, 256, size, dtype=np.uint8)
+    body[np.isin(body, np.array(sorted(ILLEGAL | {0x10}), dtype=np.uint8))] = 0x00
+    blocks = {0: bytes(body[:0x100]), 0x150: bytes(body[0x150:])}
+    envs = []  # (pc, bytes, sp)
+    for sp in EDGE_SP:
+        for op in (0xC5, 0xD5, 0xE5, 0xF5, 0xCD, 0xFF, 0xC7):
+            tgt = int(rng.integers(0x200, 0x3000))
+            envs.append((op, tgt, sp))
+    for a16 in EDGE_A16:
+        for _ in range(3):
+            envs.append((0x08, a16, int(rng.integers(0, 0x10000))))
+    n = len(envs)
+    pcs = 0x4000 - 4 * n + 4 * np.arange(n)
+    for pc, (op, k16, _) in zip(pcs, envs):
+        blocks[int(pc)] = bytes([op, k16 & 0xFF, k16 >> 8])
+    rom = flat_rom(blocks, cart_type=cart[0], rom_code=cart[1], ram_code=cart[2])
+    dut = HipVecBackend(rom, num_envs=n, frames_per_step=1, stage="full_step", bootrom=bootstub)
+    ref = RefMachine(n, rom, bootstub)
+    try:
+        dut.reset()
+        _randomize(rng, n, ref, dut, pcs)
+        sps = np.array([sp for _, _, sp in envs], np.int64)
+        ref.field("sp")[:] = sps
+        dut.import_field("sp", sps)
+        acts = rng.integers(0, 8, n).astype(np.int32)
+        assert_same_state(dut, ref, step=-1, tag=f"{cart} setup")
+        for k, tag in ((1, "1 instr"), (1, "2 instr"), (4, "6 instr")):
+            ref.set_debug(max_instr=k)
+            dut.set_debug_traps(max_instr=k)
+            ref.step(acts, 1, 8, "full_step", threads=8)
+            dut.step(acts)
+            assert_same_state(dut, ref, step=k, tag=f"{cart} {tag}")
+            _clear_traps(ref, dut)
+        ref.set_debug()
+        dut.set_debug_traps()
+        ref.step(acts, 1, 8, "full_step", threads=8)
+        dut.step(acts)
+        assert_same_state(dut, ref, step=99, tag=f"{cart} frame")
+    finally:
+        dut.close()
+        ref.close()
