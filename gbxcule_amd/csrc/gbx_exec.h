@@ -98,7 +98,7 @@ __device__ __forceinline__ ExecOut exec_insn(const Rec& r, const ExecIn& in) {
   const uint32_t t16 = sum ^ A16 ^ B16;
   const uint32_t fsv = t8 | perm(t16, XW, CIW >> 16);
   uint32_t cf = ubfe(fsv, 8, 1);
-  if (FL & (1u << 30)) {  // DAA (alu.py:897-950)
+  if (__builtin_expect((FL & (1u << 30)) != 0u, 0)) {  // DAA (alu.py:897-950)
     const uint32_t nf = (W1 >> 14) & 1u, hf = (W1 >> 13) & 1u, cin = (W1 >> 12) & 1u;
     const bool dlo = nf ? hf != 0u : (hf != 0u || (x & 15u) > 9u);
     const bool dhi = nf ? cin != 0u : (cin != 0u || x > 0x99u);

@@ -568,7 +568,7 @@ struct Lane {
   __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1) {
     const uint32_t x0 = fold(a0), x1 = fold(a1);
     const bool two = n >= 2u;
-    if (write_is_special(x0) | (two & write_is_special(x1))) {
+    if (__builtin_expect(write_is_special(x0) | (two & write_is_special(x1)), 0)) {
       write8(a0, v0);
       if (two) write8(a1, v1);
     } else {
@@ -927,10 +927,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     // pending bus writes: the instruction's, then the interrupt push
     uint32_t wn = 0, wa0 = 0, wv0 = 0, wa1 = 0, wv1 = 0;
 
-    if (!hiter) {
+    if (__builtin_expect(!hiter, 1)) {
       // ---- fetch + decode ------------------------------------------------------
       const uint32_t pc = L.pc;
-      if (!rv) {
+      if (__builtin_expect(!rv, 0)) {
         if (L.rec_ok(pc)) load_rec(L.rec_index(pc));
         else rec = L.fetch_slow();
       }
@@ -984,7 +984,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       wa1 = o.wa1;
       wv1 = o.wv1;
       uint32_t npc = o.npc;
-      if (o.misc) {  // DI EI RETI HALT, illegal opcodes, LY poll loops
+      if (__builtin_expect(o.misc != 0u, 0)) {  // DI EI RETI HALT, illegal opcodes, poll/copy loops
         if (o.misc & 1u) {
           L.ime = (o.misc >> 1) & 1u;
           L.ime_delay = 0;
@@ -1073,7 +1073,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     if (kMbc == MBC_MBC3)
       fast = fast & ((L.rtc_halt != 0u) | ((L.rtc_sub >= 0) & (L.rtc_sub + cycles < kRtcCyclesPerSecond) &
                                            (L.rtc_dirty == 0u)));
-    if (fast) {
+    if (__builtin_expect(fast, 1)) {
       L.div = (L.div + ucyc) & 0xFFFFu;
       L.scan = lcd_on ? L.scan + ucyc : 0u;
       L.stat_fresh = 0;
