@@ -961,7 +961,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
         const uint8_t* p0 = L.bus_ptr(x0);
         uint32_t x1 = x0;
         const uint8_t* p1 = p0;
-        if (nr > 1u) {
+        if (__builtin_expect(nr > 1u, 0)) {
           x1 = Lane::fold(in.ra + 1u);
           p1 = p0 + kEnvBlock;
           if ((x1 != x0 + 1u) | (x0 < 0x8000u) | (x0 - 0xA000u < 0x2000u) | (x1 - 0xA000u < 0x2000u))
@@ -1090,7 +1090,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       }
       uint32_t lcdc_now = L.ppu_advance(cycles);
       const uint32_t pending = L.ie & L.ifr & 0x1Fu;
-      if (pending) {
+      if (__builtin_expect(pending != 0u, 0)) {
         L.halted = 0;
         if (L.ime) {
           // service (cpu_step_builder.py:1502-1600): push pc, jump to the
@@ -1113,7 +1113,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           rv = false;
         }
       }
-      if (L.map_changed) {
+      if (__builtin_expect(L.map_changed != 0u, 0)) {
         L.map_changed = 0;
         rv = false;
       }
@@ -1122,7 +1122,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       L.rtc_tick(total);
       ncyc += (uint32_t)total;
       cframe += total;
-      if ((((lcdc_prev ^ lcdc_now) & 0x80u) != 0u) | (cframe >= kCyclesPerFrame)) {
+      if (__builtin_expect((((lcdc_prev ^ lcdc_now) & 0x80u) != 0u) | (cframe >= kCyclesPerFrame), 0)) {
         // LCD toggles and frame ends (cpu_step_builder.py frame loop)
         instr += ninstr;
         cyc += ncyc;
