@@ -1040,7 +1040,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
 
     // ---- write phase, debug checks, timer, PPU, interrupt check --------------
     int svc = 0;
-    if (wn) L.write_bus(wn, wa0, wv0, wa1, wv1);
+    if (__builtin_expect(wn != 0u, 1)) L.write_bus(wn, wa0, wv0, wa1, wv1);
     if (dbg) {
       if (!hiter) {
         if (dbg_rst38 && L.pc >= 0xFE00u && !trap) {
