@@ -50,7 +50,7 @@ struct ExecOut {
   uint32_t w0, w1, sp, npc;
   uint32_t cycles;
   uint32_t wn, wa0, wv0, wa1, wv1;  // bus writes, in order
-  uint32_t misc;                    // [0] IME write [1] IME value [2] HALT [3] trap [4] poll loop
+  uint32_t misc;                    // [0] IME write [1] IME value [2] HALT [3] trap [4] poll/copy loop
 };
 
 // Operand address of the bus operand (cpu_templates/loads.py address modes):

@@ -10,22 +10,24 @@
 // The implementation is not a translation of that kernel.  A wavefront runs
 // up to 64 independent instruction streams, so the loop body is built to
 // cost the same whatever mix of opcodes its lanes execute:
-//  * fetch + decode is one 8-byte load of a pre-decoded record (opcode, two
-//    operand bytes, 40-bit micro-op word, gbx_decode.h) per ROM byte, issued
-//    for the next pc while the current instruction's writes, timer and PPU
-//    work run;
-//  * execute is a single straight-line datapath driven by the micro-op
-//    fields (operand selects, one add/subtract unit shared by ADD..DEC, one
-//    shifter for every rotate, selects for the 16-bit and control ops), so no
-//    lane waits for another lane's opcode class;
-//  * bus reads compute one flat address per lane (ROM window, boot image,
+//  * fetch + decode is four 16-byte loads of the pre-decoded 64-byte record
+//    of the instruction at pc (gbx_decode.h), issued for the next pc while
+//    the current instruction's writes, timer and PPU work run;
+//  * execute is one straight-line datapath (gbx_exec.h) whose operands are
+//    byte permutes of the register file and the bus bytes selected by the
+//    record, with one shared adder, logic unit, shifter and 16-bit adder, so
+//    no lane waits for another lane's opcode class;
+//  * bus reads compute one address per lane (ROM window, boot image,
 //    cartridge RAM or the env's memory) and issue at most two loads; only IO
 //    side effects, MBC and cartridge-RAM writes take divergent branches;
 //  * CPU registers, the hot IO registers and the cartridge bank offsets live
 //    in VGPRs for the whole launch and are written back once;
-//  * a halted CPU advances in one step to the next cycle at which anything it
-//    can observe changes (a PPU mode boundary, a timer reload, the frame end),
-//    which is exactly equivalent to the reference's 4-cycle halted loop.
+//  * a halted CPU, an LY poll loop and a block-copy loop advance in one step
+//    to the first event the reference's per-instruction loop could observe
+//    (ff_horizon), which is exactly equivalent to stepping them one
+//    instruction (or 4 halted cycles) at a time;
+//  * the rare paths carry branch-probability hints so that the common path
+//    is laid out as straight fall-through code.
 #include "gbx_internal.h"
 // after gbx_internal.h, which brings in the HIP runtime
 #include "gbx_exec.h"
