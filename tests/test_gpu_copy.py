@@ -21,6 +21,7 @@ from gbxcule_amd.carts.asm import Asm
 from gbxcule_amd.carts.synth import PROGRAM_ORIGIN, _vectors, finalize_rom, seeded_actions
 from oracle.ref import RefMachine
 
+from ._isa import CS_BOOT
 from ._parity import assert_same_state
 from .conftest import require_gpu
 
@@ -167,6 +168,58 @@ def test_copy_loop_parity(bootstub, seed, ime, ie, tac, stat, lcd_off, mbc1):
         if ime and ie & 2 and stat & 0x08:
             assert int(mem[0, 0xDF01]) > 0  # HBlank STAT interrupts were serviced
         assert int(ref.field("trap_flag").sum()) == 0
+    finally:
+        dut.close()
+        ref.close()
+
+
+def test_copy_loop_under_boot_overlay():
+    """A boot image that hands over without unmapping itself: the cart's
+    copy loops read 0x0000-0x0107 through the overlay (the boot image, then
+    the cart past 0x00FF), which is never batched, and then unmap it."""
+    require_gpu()
+    from gbxcule_amd.backend import HipVecBackend
+
+    boot_asm = Asm(origin=0x0000)
+    boot_asm.ld_rr_d16("SP", 0xFFFE)
+    boot_asm.jp(0x0100)
+    boot = bytearray(boot_asm.resolve())
+    boot.extend(bytes((0x40 + i) & 0xFF for i in range(0x100 - len(boot))))  # read through the overlay
+    rng = np.random.default_rng(11)
+    rom = bytearray(0x8000)
+    rom[0x0000:0x0100] = rng.integers(0, 256, 0x100, dtype=np.uint8).tobytes()  # hidden while mapped
+    rom[0x1000:0x4000] = rng.integers(0, 256, 0x3000, dtype=np.uint8).tobytes()
+    a = Asm(origin=PROGRAM_ORIGIN)
+    a.ld_rr_d16("SP", 0xDFF0)
+    a.label("loop")
+    _copy(a, 0x0000, 0xC000, 0x108, "c_boot")  # boot image, then cart bytes
+    _copy(a, 0x00F0, 0xC200, 0x40, "c_edge")
+    _copy(a, 0x1000, 0xC400, 0x200, "c_rom")
+    a.ld_a_a16(0xDE80)
+    a.inc_r("A")
+    a.ld_a16_a(0xDE80)
+    a.alu_d8("AND", 0x07)
+    a.jr("loop", "NZ")
+    a.ld_r_d8("A", 0x01)
+    a.ldh_a8_a(0x50)  # unmap the boot image; later passes read the cart
+    a.jp("loop")
+    code = a.resolve()
+    rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
+    rom = finalize_rom(rom, "GBXAMD BOOTCP", 0x00, 0x00, 0x00)
+    n, fs = 64, 24
+    dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
+                        stage="emulate_only", bootrom=bytes(boot))  # fmt: skip
+    ref = RefMachine(n, rom, bytes(boot))
+    try:
+        dut.reset(seed=11)
+        ref.step(None, 0, 0, "emulate_only")
+        for k in range(3):
+            act = seeded_actions(11, k, n)
+            dut.step(act)
+            ref.step(act, fs, 8, "emulate_only", threads=8)
+            assert_same_state(dut, ref, step=k, tag="bootcopy")
+        assert int(ref.mem[0, 0xDE80]) > 8  # ran before and after the unmap
+        assert int(ref.cart_state[0, CS_BOOT]) == 0
     finally:
         dut.close()
         ref.close()
