@@ -956,22 +956,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       in.rd0 = 0;
       in.rd1 = 0;
       if (nr) {
-        // Both loads issue before either is used.  The second byte (POP,
-        // RET) sits one address row (64 bytes) after the first when both
-        // are in the env's memory; a lane with one read repeats its first.
+        // A second load only for two-byte reads (POP, RET), issued before
+        // either byte is used; that byte sits one address row (64 bytes)
+        // after the first when both are in the env's memory.  A lane with
+        // one read repeats its first byte.
         const uint32_t x0 = Lane::fold(in.ra);
         const uint8_t* p0 = L.bus_ptr(x0);
-        uint32_t x1 = x0;
-        const uint8_t* p1 = p0;
+        const uint32_t v0 = ld_global(p0);
+        uint32_t x1 = x0, v1 = 0;
         if (__builtin_expect(nr > 1u, 0)) {
           x1 = Lane::fold(in.ra + 1u);
-          p1 = p0 + kEnvBlock;
+          const uint8_t* p1 = p0 + kEnvBlock;
           if ((x1 != x0 + 1u) | (x0 < 0x8000u) | (x0 - 0xA000u < 0x2000u) | (x1 - 0xA000u < 0x2000u))
             p1 = L.bus_ptr(x1);
+          v1 = ld_global(p1);
         }
-        const uint32_t v0 = ld_global(p0), v1 = ld_global(p1);
         in.rd0 = L.bus_fix(x0, v0);
-        in.rd1 = L.bus_fix(x1, v1);
+        in.rd1 = nr > 1u ? L.bus_fix(x1, v1) : in.rd0;
       }
 
       // ---- execute (gbx_exec.h) -------------------------------------------------
