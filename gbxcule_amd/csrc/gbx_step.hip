@@ -275,7 +275,7 @@ struct Lane {
       v = (cart & !ram_ok) ? 0xFFu : v;  // no RTC: disabled RAM reads 0xFF
     }
     v = x == 0xFF04u ? ff04_val() : v;
-    if (x == 0xFF41u) v = stat_val();
+    if (__builtin_expect(x == 0xFF41u, 0)) v = stat_val();
     return v;
   }
   __device__ uint32_t read8(uint32_t addr) const {
