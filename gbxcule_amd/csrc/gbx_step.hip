@@ -556,7 +556,8 @@ struct Lane {
   // A write that is not a plain store to the env's memory: MBC registers,
   // cartridge RAM, IO bytes with side effects.
   __device__ static bool write_is_special(uint32_t x) {
-    return (x < 0x8000u) | (x - 0xA000u < 0x2000u) | io_special(x);
+    // 4 KiB regions 0-7 (MBC registers) and A-B (cartridge RAM); x < 0x10000
+    return (((0x0CFFu >> (x >> 12)) & 1u) != 0u) | io_special(x);
   }
   __device__ void write8(uint32_t addr, uint32_t v) {
     const uint32_t x = fold(addr);
