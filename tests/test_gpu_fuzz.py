@@ -5,9 +5,10 @@ Each seed builds a cart whose main loop runs a block of random legal code
 (CB included, joypad-keyed branches, stores into work RAM), an LY poll loop
 with a random condition and line, a block-copy loop between random windows
 with a random length (overlaps and window edges included), and optionally a
-HALT wait, under a random timer rate, STAT source set, IE mask and IME.
-The random code itself may write IO registers.  State is compared in full
-after every step.
+HALT wait, under a random timer rate, STAT source set, IE mask and IME, on
+ROM-only, MBC1 and MBC3 (cart RAM, RTC) carts whose loops also switch banks.
+The random code itself may write IO registers (and MBC3 cart RAM).  State
+is compared in full after every step.
 """
 
 from __future__ import annotations
@@ -39,11 +40,14 @@ _SRC = [(0x0100, 0x3F00), (0x3F80, 0x4000), (0x4000, 0x7F00), (0x8000, 0x9F00), 
 _DST = [(0x8000, 0x9F00), (0x9FC0, 0xA000), (0xC000, 0xDC00), (0xFE00, 0xFE80)]
 
 
-def fuzz_cart(seed: int) -> bytes:
+def fuzz_cart(seed: int, mbc: int = 0) -> bytes:
+    """ROM-only (mbc 0), MBC1 with 4 banks (1) or MBC3 with 4 banks and
+    32 KiB of cart RAM (3)."""
     rng = np.random.default_rng(seed)
     r = lambda lo, hi: int(rng.integers(lo, hi))  # noqa: E731
-    rom = bytearray(0x8000)
-    rom[0x1000:0x8000] = rng.integers(0, 256, 0x7000, dtype=np.uint8).tobytes()
+    size = 0x8000 if mbc == 0 else 0x10000
+    rom = bytearray(size)
+    rom[0x1000:size] = rng.integers(0, 256, size - 0x1000, dtype=np.uint8).tobytes()
     h = Asm(origin=0x0068)
     for name, counter in (("vbl", 0xDF00), ("stat", 0xDF01), ("timer", 0xDF02)):
         h.label(name)
@@ -60,6 +64,9 @@ def fuzz_cart(seed: int) -> bytes:
 
     a = Asm(origin=PROGRAM_ORIGIN)
     a.ld_rr_d16("SP", 0xDFF0)
+    if mbc == 3:
+        a.ld_r_d8("A", 0x0A)
+        a.ld_a16_a(0x0000)  # cart RAM and RTC on
     for reg, val in ((0x06, r(0, 256)), (0x07, r(0, 8)), (0x45, r(0, 154)),
                      (0x41, int(rng.choice([0x00, 0x08, 0x10, 0x20, 0x40, 0x48, 0x50, 0x78]))),
                      (0xFF, r(0, 32)), (0x0F, 0x00)):  # fmt: skip
@@ -70,10 +77,24 @@ def fuzz_cart(seed: int) -> bytes:
     a.ld_r_d8("A", 0x91)
     a.ldh_a8_a(0x40)
     a.label("loop")
-    for part in rng.permutation(4):
-        if part == 0:  # random code
+    for part in rng.permutation(5):
+        if part == 4:  # the ROM bank from the joypad; an MBC3 RAM bank or RTC register
+            if mbc:
+                a.ld_r_d8("A", 0x10)
+                a.ldh_a8_a(0x00)
+                a.ldh_a_a8(0x00)
+                a.alu_d8("AND", 0x03)
+                a.ld_a16_a(0x2000)
+            if mbc == 3:
+                a.ld_r_d8("A", int(rng.choice([0, 1, 2, 3, 8, 9, 0xC])))
+                a.ld_a16_a(0x4000)
+                a.ld_r_d8("A", 0x00)
+                a.ld_a16_a(0x6000)
+                a.ld_r_d8("A", 0x01)
+                a.ld_a16_a(0x6000)  # latch the RTC
+        elif part == 0:  # random code
             gen = CodeGen(rng, a, stack="reseed", joypad_conditions=True, store_lo=0xC000,
-                          store_hi=0xDDFF)  # fmt: skip
+                          store_hi=0xDDFF, cart_ram=mbc == 3)  # fmt: skip
             _emit_random_program(gen, r(24, 96), LEGAL_NON_CB + _cb_pool())
             end = a.pc
             gen.resolve(end)
@@ -116,15 +137,17 @@ def fuzz_cart(seed: int) -> bytes:
     code = a.resolve()
     assert PROGRAM_ORIGIN + len(code) < 0x1000
     rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
-    return finalize_rom(rom, "GBXAMD FUZZ", 0x00, 0x00, 0x00)
+    kind = {0: (0x00, 0x00, 0x00), 1: (0x01, 0x01, 0x00), 3: (0x10, 0x01, 0x03)}[mbc]
+    return finalize_rom(rom, "GBXAMD FUZZ", *kind)
 
 
-@pytest.mark.parametrize("seed", range(100, 112))
-def test_fuzz_parity(bootstub, seed):
+@pytest.mark.parametrize("seed,mbc", [(s, 0) for s in range(100, 112)] + [(s, 1) for s in range(120, 124)]
+                         + [(s, 3) for s in range(130, 134)])  # fmt: skip
+def test_fuzz_parity(bootstub, seed, mbc):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
 
-    rom = fuzz_cart(seed)
+    rom = fuzz_cart(seed, mbc)
     n, fs, steps = 64, 24, 3
     dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
                         stage="emulate_only", bootrom=bootstub)  # fmt: skip
