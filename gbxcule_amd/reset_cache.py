@@ -16,7 +16,6 @@ from typing import Any
 
 import numpy as np
 
-from . import _lib
 from .backend import HipVecBackend, _cur_stream, _torch
 
 
