@@ -156,6 +156,7 @@ struct Lane {
   int rtc_sub;
   uint32_t rtc_halt, rtc_dirty;
   uint32_t map_changed;  // set when a write remaps the fetch windows
+  int budget;            // cycles a fast-path step may take (event_budget)
   // frame loop
   int frames_done, release;
   int32_t action;
@@ -428,6 +429,7 @@ struct Lane {
     return (x >= 0xFF00u) & ((k == 0xFFu) | (((m >> (k & 31u)) & 1u) != 0u));
   }
   __device__ void io_write(uint32_t x, uint32_t v) {
+    budget = 0;  // timer, LCD and PPU registers feed event_budget
     const uint32_t k = x & 0xFFu;
     // plain register copies
     tima = sel(k == 0x05u, v, tima);
@@ -772,6 +774,17 @@ struct Lane {
         if (j + t < k) M(dst + (uint32_t)(j + t)) = v[t];
     }
   }
+  // Cycles a step may take on the fast path: it must not reach a TIMA
+  // edge, the scanline end or the frame end (0 while a switched-off LCD still
+  // has PPU state to clear).
+  __device__ int event_budget(int cframe) const {
+    int b = kCyclesPerFrame - cframe;
+    const uint32_t te = tmask - (div & 0xFFFFu & tmask);
+    b = te < (uint32_t)b ? (int)te + 1 : b;
+    if (lcdc & 0x80u) b = min(b, kCyclesPerLine - (int)scan);
+    else if ((scan | ly | wl | lym) != 0u) b = 0;
+    return b;
+  }
   // Cycles a halted CPU advances in one loop iteration: the reference steps
   // 4 cycles at a time and wakes on IE & IF; nothing it can observe changes
   // before the first event of ff_horizon for the requests IE enables, so it
@@ -867,6 +880,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   L.rtc_halt = (L.CS(CS_RTC_DAYS_HIGH) & 0x40) ? 1u : 0u;
   L.rtc_dirty = 1;  // first tick of a launch normalizes like the reference does
   L.map_changed = 0;
+  L.budget = 0;
   L.refresh_cart();
   L.action = args.actions[e];
   L.release = (int)in_vgpr((uint32_t)args.release);
@@ -1069,11 +1083,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     const uint32_t lc_now = L.lcdc;
     const uint32_t ucyc = (uint32_t)cycles;
     const bool lcd_on = (lc_now & 0x80u) != 0u;
-    bool fast = (trap == 0) & (L.pend == 0u) & (((L.div & 0xFFFFu & L.tmask) + ucyc) <= L.tmask) &
-                (L.ime_delay == 0u) & ((L.ie & L.ifr & 0x1Fu) == 0u) & (L.map_changed == 0u) &
-                (((lcdc_prev ^ lc_now) & 0x80u) == 0u) & (cframe + cycles < kCyclesPerFrame) &
-                ((lcd_on & (L.scan + ucyc < (uint32_t)kCyclesPerLine)) |
-                 (!lcd_on & ((L.scan | L.ly | L.wl | L.lym) == 0u)));
+    bool fast = (trap == 0) & (L.pend == 0u) & (cycles < L.budget) & (L.ime_delay == 0u) &
+                ((L.ie & L.ifr & 0x1Fu) == 0u) & (L.map_changed == 0u) & (((lcdc_prev ^ lc_now) & 0x80u) == 0u);
     if (kMbc == MBC_MBC3)
       fast = fast & ((L.rtc_halt != 0u) | ((L.rtc_sub >= 0) & (L.rtc_sub + cycles < kRtcCyclesPerSecond) &
                                            (L.rtc_dirty == 0u)));
@@ -1086,6 +1097,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       if (kMbc == MBC_MBC3) L.rtc_sub += L.rtc_halt ? 0 : cycles;
       ncyc += ucyc;
       cframe += cycles;
+      L.budget -= cycles;
     } else if (!trap) {
       L.timer_tick(cycles);
       if (!hiter & (L.ime_delay != 0u)) {
@@ -1161,6 +1173,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           L.joyp_refresh();
         }
       }
+      L.budget = L.event_budget(cframe);
     }
   }
   instr += ninstr;
