@@ -1,6 +1,8 @@
 // gbx_aux.hip -- kernels around the step: power-on fill, the 2x-downsampled
 // snapshot renderer, reset snapshot / masked restore, RAM-sense gather, state
 // hash, and the layout converters behind the export/import helpers.
+#include <utility>
+
 #include "gbx_aux.h"
 
 namespace gbx {
@@ -62,36 +64,158 @@ __device__ uint32_t bg_tile_addr(uint32_t lcdc, uint32_t tile_id) {
   return (uint32_t)(0x9000 + ((int)tile_id >= 128 ? (int)tile_id - 256 : (int)tile_id) * 16);
 }
 
-constexpr int kRenderThreads = 128;
+constexpr int kRenderRows = 4;  // output rows per workgroup, one wavefront each
+constexpr int kRenderThreads = kEnvBlock * kRenderRows;
+constexpr int kTileSlots = 21;  // tile columns one 80-sample row can touch
 
+// One BG or window layer of a row, for a layer whose sample x reads map pixel
+// px = (x + s) & 0xFF (s = SCX for the background, 7 - WX for the window):
+// w[j] = lo | hi << 8 of the tile row of map column ((s >> 3) + j) & 31, so
+// sample x uses slot (x + (s & 7)) >> 3 and bit 7 - ((x + s) & 7).  The 21
+// map reads are independent, then the 42 tile-data reads are.
+__device__ __forceinline__ void load_layer(const Row& r, uint32_t lcdc, uint32_t map, uint32_t s,
+                                           uint32_t py, uint32_t (&w)[kTileSlots]) {
+  const uint32_t mrow = map + (py >> 3) * 32u;
+  uint32_t id[kTileSlots];
+#pragma unroll
+  for (int j = 0; j < kTileSlots; ++j) id[j] = r.M(mrow + (((s >> 3) + (uint32_t)j) & 31u));
+  const uint32_t row2 = (py & 7u) * 2u;
+#pragma unroll
+  for (int j = 0; j < kTileSlots; ++j) {
+    const uint32_t ta = bg_tile_addr(lcdc, id[j]) + row2;
+    w[j] = r.M(ta) | (r.M(ta + 1u) << 8);
+  }
+}
+
+// Colour (0..3) of sample ox of a layer: slot ox >> 2 or the next one, as
+// 2 * (ox & 3) + (s & 7) crosses a tile edge.
+template <int ox>
+__device__ __forceinline__ uint32_t layer_color(const uint32_t (&w)[kTileSlots], uint32_t s) {
+  constexpr int j = ox >> 2;
+  const uint32_t s7 = s & 7u;
+  // both slots read unconditionally and blended, so the slot arrays stay in
+  // registers (a select of the two elements would load through a pointer)
+  uint32_t t = w[j];
+  if constexpr (j + 1 < kTileSlots) t ^= (t ^ w[j + 1]) & (0u - (uint32_t)(2u * (ox & 3) + s7 >= 8u));
+  const uint32_t bit = 7u - ((2u * ox + s7) & 7u);
+  return ((t >> bit) & 1u) | ((t >> (bit + 7u)) & 2u);
+}
+
+template <int ox>
+__device__ __forceinline__ void render_sample(const uint32_t (&wb)[kTileSlots], const uint32_t (&ww)[kTileSlots],
+                                              uint32_t lcdc, uint32_t scx, uint32_t sw, bool win, int wx7,
+                                              uint32_t bgp, uint32_t obp0, uint32_t obp1, bool sprites,
+                                              const uint16_t (&line)[kDsW][kEnvBlock], uint32_t lane,
+                                              uint32_t& word, uint8_t* dst, bool aligned, bool live,
+                                              int packed) {
+  uint32_t shade = 0, bg_color = 0;
+  if (lcdc & 0x01u) {
+    const bool in_win = win && 2 * ox >= wx7;
+    const uint32_t cw = layer_color<ox>(ww, sw), cb = layer_color<ox>(wb, scx);
+    bg_color = in_win ? cw : cb;
+    shade = (bgp >> (bg_color * 2u)) & 3u;
+  }
+  if (sprites) {
+    const uint32_t o = line[ox][lane];
+    if (o != 0u && !(((o >> 11) & 1u) && bg_color != 0)) {
+      const uint32_t pal = ((o >> 10) & 1u) ? obp1 : obp0;
+      shade = (pal >> (((o >> 8) & 3u) * 2u)) & 3u;
+    }
+  }
+  if (packed) {
+    word |= shade << (2u * (ox & 3) + 8u * ((ox >> 2) & 3));
+    if constexpr ((ox & 15) == 15 || ox == kDsW - 1) {
+      constexpr int b0 = (ox >> 2) & ~3;  // first byte of this word
+      constexpr int nb = (ox >> 2) - b0 + 1;
+      if (live) {
+        if (aligned && nb == 4) {
+          *reinterpret_cast<uint32_t*>(dst + b0) = word;
+        } else {
+#pragma unroll
+          for (int q = 0; q < nb; ++q) dst[b0 + q] = (uint8_t)(word >> (8 * q));
+        }
+      }
+      word = 0;
+    }
+  } else {
+    word |= shade << (8u * (ox & 3));
+    if constexpr ((ox & 3) == 3) {
+      if (live) {
+        if (aligned) {
+          *reinterpret_cast<uint32_t*>(dst + (ox & ~3)) = word;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dst[(ox & ~3) + q] = (uint8_t)(word >> (8 * q));
+        }
+      }
+      word = 0;
+    }
+  }
+}
+
+template <int... ox>
+__device__ __forceinline__ void render_row(std::integer_sequence<int, ox...>, const uint32_t (&wb)[kTileSlots],
+                                           const uint32_t (&ww)[kTileSlots], uint32_t lcdc, uint32_t scx,
+                                           uint32_t sw, bool win, int wx7, uint32_t bgp, uint32_t obp0,
+                                           uint32_t obp1, bool sprites, const uint16_t (&line)[kDsW][kEnvBlock],
+                                           uint32_t lane, uint8_t* dst, bool aligned, bool live, int packed) {
+  uint32_t word = 0;
+  (render_sample<ox>(wb, ww, lcdc, scx, sw, win, wx7, bgp, obp0, obp1, sprites, line, lane, word, dst, aligned,
+                     live, packed),
+   ...);
+}
+
+// One workgroup per 64-env memory block and 4 output rows; lanes are the
+// block's envs, so every read of one address by a wavefront is one 64-byte
+// row.  The block's OAM is staged into LDS once for the 4 rows.  Per row, the
+// sprites (the first 10 OAM entries overlapping the line, counted before the
+// x test) are resolved into a line buffer of the 80 samples: each sample
+// keeps the opaque sprite pixel with the lowest x (ties: the lower OAM index,
+// the earlier entry), as the reference's per-sample search over OAM selects
+// it.  The BG and window tile rows are fetched for all 21 tile columns at
+// once, then the 80 samples are shaded from registers.
 __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
                                                                 int packed) {
-  // line buffer, one column per thread: 0 = no sprite pixel, else bit 15 set,
-  // [0:7] the sprite's OAM x (its left edge + 8), [8:9] colour, [10] OBP1,
-  // [11] behind non-zero BG
-  __shared__ uint16_t obj[kDsW][kRenderThreads];
-  const uint32_t t = threadIdx.x;
-  const uint32_t e = blockIdx.x * kRenderThreads + t;
-  const uint32_t oy = blockIdx.y;
-  if (e >= (uint32_t)s.n) return;
-  Row r{s.mem + ((size_t)block_of(e) << 22), e & (kEnvBlock - 1)};
+  // OAM entry k of each env: y | x << 8 | tile << 16 | attr << 24
+  __shared__ uint32_t oam[40][kEnvBlock];
+  // sprite line buffer per row: 0 = no sprite pixel, else bit 15 set, [0:7]
+  // the sprite's OAM x (its left edge + 8), [8:9] colour, [10] OBP1, [11]
+  // behind non-zero BG
+  __shared__ uint16_t obj[kRenderRows][kDsW][kEnvBlock];
+  const uint32_t lane = threadIdx.x & (kEnvBlock - 1);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> kEnvBlockShift);
+  const uint32_t blk = blockIdx.x;
+  const uint32_t e = blk * kEnvBlock + lane;
+  const bool live = e < (uint32_t)s.n;  // the block's spare lanes render but never store
+  const Row r{s.mem + ((size_t)blk << 22), lane};
+#pragma unroll
+  for (int i = 0; i < 40 / kRenderRows; ++i) {
+    const uint32_t k = wv + (uint32_t)(kRenderRows * i);
+    const uint32_t a = 0xFE00u + 4u * k;
+    oam[k][lane] = r.M(a) | (r.M(a + 1u) << 8) | (r.M(a + 2u) << 16) | (r.M(a + 3u) << 24);
+  }
+  const uint32_t oy = blockIdx.y * kRenderRows + wv;
   const uint32_t y = oy * 2u;
   const uint32_t lcdc = r.M(0xFF40), scy = r.M(0xFF42), scx = r.M(0xFF43);
   const uint32_t bgp = r.M(0xFF47), obp0 = r.M(0xFF48), obp1 = r.M(0xFF49);
   const uint32_t wy = r.M(0xFF4A), wx = r.M(0xFF4B);
   const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
   const bool sprites = (lcdc & 0x02u) != 0u;
+  uint16_t (&line)[kDsW][kEnvBlock] = obj[wv];
+  __syncthreads();
   if (sprites) {
-    for (int ox = 0; ox < kDsW; ++ox) obj[ox][t] = 0;
+#pragma unroll
+    for (int ox = 0; ox < kDsW; ++ox) line[ox][lane] = 0;
     uint32_t on_line = 0;
     for (uint32_t k = 0; k < 40u && on_line < 10u; ++k) {
-      const uint32_t sy = r.M(0xFE00u + 4u * k), sx = r.M(0xFE01u + 4u * k);
+      const uint32_t ent = oam[k][lane];
+      const uint32_t sy = ent & 0xFFu, sx = (ent >> 8) & 0xFFu;
       if (sx == 0 || sy == 0 || sx >= 168u || sy >= 160u) continue;
       const int top = (int)sy - 16;
       if ((int)y < top || (int)y >= top + (int)height) continue;
       ++on_line;
-      uint32_t tile = r.M(0xFE02u + 4u * k);
-      const uint32_t attr = r.M(0xFE03u + 4u * k);
+      uint32_t tile = (ent >> 16) & 0xFFu;
+      const uint32_t attr = ent >> 24;
       uint32_t row = (uint32_t)((int)y - top);
       if ((attr >> 6) & 1u) row = height - 1u - row;
       if (height == 16u) {
@@ -112,76 +236,29 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
         const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
         const uint32_t color = (((hi >> bit) & 1u) << 1) | ((lo >> bit) & 1u);
         if (color == 0) continue;
-        const uint32_t cur = obj[x >> 1][t];
-        if (cur == 0 || sx < (cur & 0xFFu)) obj[x >> 1][t] = (uint16_t)(tag | (color << 8));
+        const uint32_t cur = line[x >> 1][lane];
+        if (cur == 0 || sx < (cur & 0xFFu)) line[x >> 1][lane] = (uint16_t)(tag | (color << 8));
       }
     }
   }
   const bool win = (lcdc & 0x20u) && y >= wy;
-  const uint32_t bg_map = (lcdc & 0x08u) ? 0x9C00u : 0x9800u;
-  const uint32_t win_map = (lcdc & 0x40u) ? 0x9C00u : 0x9800u;
-  uint32_t word = 0;
-  uint32_t tkey = 0xFFFFFFFFu, tlo = 0, thi = 0;
+  const int wx7 = (int)wx - 7;
+  const uint32_t sw = (7u - wx) & 0xFFu;  // window: px = (x - (WX - 7)) & 0xFF
+  uint32_t wb[kTileSlots], ww[kTileSlots];
+#pragma unroll
+  for (int j = 0; j < kTileSlots; ++j) wb[j] = ww[j] = 0;
+  if (lcdc & 0x01u) {
+    // the background unless the window covers the whole row
+    if (!(win && wx7 <= 0))
+      load_layer(r, lcdc, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, (y + scy) & 0xFFu, wb);
+    if (win && wx7 < 2 * kDsW - 1)
+      load_layer(r, lcdc, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, (y - wy) & 0xFFu, ww);
+  }
   uint8_t* dst = out + base + (size_t)e * (packed ? (size_t)kDsWB * kDsH : (size_t)kDsW * kDsH) +
                  (size_t)oy * (packed ? kDsWB : kDsW);
   const bool aligned = (((uintptr_t)dst) & 3u) == 0;
-  for (int ox = 0; ox < kDsW; ++ox) {
-    const uint32_t x = (uint32_t)ox * 2u;
-    uint32_t shade = 0, bg_color = 0;
-    if (lcdc & 0x01u) {
-      uint32_t px, py, map;
-      if (win && (int)x >= (int)wx - 7) {
-        px = (x - (wx - 7u)) & 0xFFu;
-        py = (y - wy) & 0xFFu;
-        map = win_map;
-      } else {
-        px = (x + scx) & 0xFFu;
-        py = (y + scy) & 0xFFu;
-        map = bg_map;
-      }
-      // py is fixed within each of the two regions; the tile follows the
-      // map entry and the row within the tile
-      const uint32_t maddr = map + (py >> 3) * 32u + (px >> 3);
-      const uint32_t key = maddr | ((py & 7u) << 16);
-      if (key != tkey) {
-        const uint32_t ta = bg_tile_addr(lcdc, r.M(maddr)) + (py & 7u) * 2u;
-        tlo = r.M(ta);
-        thi = r.M(ta + 1u);
-        tkey = key;
-      }
-      const uint32_t bit = 7u - (px & 7u);
-      bg_color = (((thi >> bit) & 1u) << 1) | ((tlo >> bit) & 1u);
-      shade = (bgp >> (bg_color * 2u)) & 3u;
-    }
-    if (sprites) {
-      const uint32_t o = obj[ox][t];
-      if (o != 0u && !(((o >> 11) & 1u) && bg_color != 0)) {
-        const uint32_t pal = ((o >> 10) & 1u) ? obp1 : obp0;
-        shade = (pal >> (((o >> 8) & 3u) * 2u)) & 3u;
-      }
-    }
-    if (packed) {
-      word |= shade << (2u * (ox & 3) + 8u * ((ox >> 2) & 3));
-      if ((ox & 15) == 15 || ox == kDsW - 1) {
-        const int b0 = (ox >> 2) & ~3;  // first byte of this word
-        const int nb = (ox >> 2) - b0 + 1;
-        if (aligned && nb == 4) {
-          *reinterpret_cast<uint32_t*>(dst + b0) = word;
-        } else {
-          for (int q = 0; q < nb; ++q) dst[b0 + q] = (uint8_t)(word >> (8 * q));
-        }
-        word = 0;
-      }
-    } else {
-      word |= shade << (8u * (ox & 3));
-      if ((ox & 3) == 3) {
-        if (aligned) *reinterpret_cast<uint32_t*>(dst + (ox & ~3)) = word;
-        else
-          for (int q = 0; q < 4; ++q) dst[(ox & ~3) + q] = (uint8_t)(word >> (8 * q));
-        word = 0;
-      }
-    }
-  }
+  render_row(std::make_integer_sequence<int, kDsW>{}, wb, ww, lcdc, scx, sw, win, wx7, bgp, obp0, obp1, sprites,
+             line, lane, dst, aligned, live, packed);
 }
 
 // ---------------------------------------------------------------------------
@@ -459,7 +536,7 @@ hipError_t launch_render_bg_env0(const DevState& s, uint8_t* out, hipStream_t st
 hipError_t launch_render(const DevState& s, uint8_t* out, int64_t base, int packed,
                          hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(render_kernel, dim3((unsigned)((s.n + kRenderThreads - 1) / kRenderThreads), kDsH),
+  hipLaunchKernelGGL(render_kernel, dim3((unsigned)(s.npad / kEnvBlock), kDsH / kRenderRows),
                      dim3(kRenderThreads), 0, st, s, out, base, packed);
   return hipGetLastError();
 }
