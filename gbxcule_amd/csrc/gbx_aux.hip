@@ -66,15 +66,30 @@ __device__ uint32_t bg_tile_addr(uint32_t lcdc, uint32_t tile_id) {
 
 constexpr int kRenderRows = 4;  // output rows per workgroup, one wavefront each
 constexpr int kRenderThreads = kEnvBlock * kRenderRows;
-constexpr int kTileSlots = 21;  // tile columns one 80-sample row can touch
+constexpr int kTileSlots = 21;          // tile columns one 80-sample row can touch
+constexpr int kGroups = kDsW / 4;       // 4-sample groups per row (one output word unpacked)
+
+// The four sampled pixels of one tile row word t = lo | hi << 8, colours
+// (0..3) one per byte, byte i = the i-th sampled pixel from the left: bits
+// 7-p, 5-p, 3-p, 1-p, where p is the layer's sample phase.  After the bit
+// reverse, lo bit 7-p-2i sits at 24+p+2i and hi bit 7-p-2i at 16+p+2i, so u
+// holds colour i at bits 2i..2i+1; the two multiplies spread the even and the
+// odd colours to bytes without overlapping terms.
+__device__ __forceinline__ uint32_t spread_tile(uint32_t t, uint32_t p) {
+  const uint32_t r = __builtin_bitreverse32(t);
+  const uint32_t u = ((r >> (24u + p)) & 0x55u) | ((r >> (15u + p)) & 0xAAu);
+  const uint32_t ev = ((u & 0x33u) * 0x1001u) & 0x00030003u;   // colours 0, 2 -> bytes 0, 2
+  const uint32_t od = ((u & 0xCCu) * 0x40040u) & 0x03000300u;  // colours 1, 3 -> bytes 1, 3
+  return ev | od;
+}
 
 // One BG or window layer of a row, for a layer whose sample x reads map pixel
 // px = (x + s) & 0xFF (s = SCX for the background, 7 - WX for the window):
-// w[j] = lo | hi << 8 of the tile row of map column ((s >> 3) + j) & 31, so
-// sample x uses slot (x + (s & 7)) >> 3 and bit 7 - ((x + s) & 7).  The 21
-// map reads are independent, then the 42 tile-data reads are.
+// c[j] = the sampled colours (spread_tile) of map column ((s >> 3) + j) & 31.
+// Sample ox is then byte ox + ((s & 7) >> 1) of the byte stream c[0], c[1], ...
+// The 21 map reads are independent, then the 42 tile-data reads are.
 __device__ __forceinline__ void load_layer(const Row& r, uint32_t lcdc, uint32_t map, uint32_t s,
-                                           uint32_t py, uint32_t (&w)[kTileSlots]) {
+                                           uint32_t py, uint32_t (&c)[kTileSlots]) {
   const uint32_t mrow = map + (py >> 3) * 32u;
   uint32_t id[kTileSlots];
 #pragma unroll
@@ -83,86 +98,31 @@ __device__ __forceinline__ void load_layer(const Row& r, uint32_t lcdc, uint32_t
 #pragma unroll
   for (int j = 0; j < kTileSlots; ++j) {
     const uint32_t ta = bg_tile_addr(lcdc, id[j]) + row2;
-    w[j] = r.M(ta) | (r.M(ta + 1u) << 8);
+    c[j] = spread_tile(r.M(ta) | (r.M(ta + 1u) << 8), s & 1u);
   }
 }
 
-// Colour (0..3) of sample ox of a layer: slot ox >> 2 or the next one, as
-// 2 * (ox & 3) + (s & 7) crosses a tile edge.
-template <int ox>
-__device__ __forceinline__ uint32_t layer_color(const uint32_t (&w)[kTileSlots], uint32_t s) {
-  constexpr int j = ox >> 2;
-  const uint32_t s7 = s & 7u;
-  // both slots read unconditionally and blended, so the slot arrays stay in
-  // registers (a select of the two elements would load through a pointer)
-  uint32_t t = w[j];
-  if constexpr (j + 1 < kTileSlots) t ^= (t ^ w[j + 1]) & (0u - (uint32_t)(2u * (ox & 3) + s7 >= 8u));
-  const uint32_t bit = 7u - ((2u * ox + s7) & 7u);
-  return ((t >> bit) & 1u) | ((t >> (bit + 7u)) & 2u);
-}
-
-template <int ox>
-__device__ __forceinline__ void render_sample(const uint32_t (&wb)[kTileSlots], const uint32_t (&ww)[kTileSlots],
-                                              uint32_t lcdc, uint32_t scx, uint32_t sw, bool win, int wx7,
-                                              uint32_t bgp, uint32_t obp0, uint32_t obp1, bool sprites,
-                                              const uint16_t (&line)[kDsW][kEnvBlock], uint32_t lane,
-                                              uint32_t& word, uint8_t* dst, bool aligned, bool live,
-                                              int packed) {
-  uint32_t shade = 0, bg_color = 0;
-  if (lcdc & 0x01u) {
-    const bool in_win = win && 2 * ox >= wx7;
-    const uint32_t cw = layer_color<ox>(ww, sw), cb = layer_color<ox>(wb, scx);
-    bg_color = in_win ? cw : cb;
-    shade = (bgp >> (bg_color * 2u)) & 3u;
-  }
-  if (sprites) {
-    const uint32_t o = line[ox][lane];
-    if (o != 0u && !(((o >> 11) & 1u) && bg_color != 0)) {
-      const uint32_t pal = ((o >> 10) & 1u) ? obp1 : obp0;
-      shade = (pal >> (((o >> 8) & 3u) * 2u)) & 3u;
-    }
-  }
-  if (packed) {
-    word |= shade << (2u * (ox & 3) + 8u * ((ox >> 2) & 3));
-    if constexpr ((ox & 15) == 15 || ox == kDsW - 1) {
-      constexpr int b0 = (ox >> 2) & ~3;  // first byte of this word
-      constexpr int nb = (ox >> 2) - b0 + 1;
-      if (live) {
-        if (aligned && nb == 4) {
-          *reinterpret_cast<uint32_t*>(dst + b0) = word;
-        } else {
+// Store one output row of the block's 64 envs from the staging area: lanes
+// run along each env's row (W words), so one store instruction covers about
+// 64*4/(4*W) envs' rows instead of 64 rows 5,760 bytes apart.
+template <int W>
+__device__ __forceinline__ void store_rows(const uint32_t* stage, uint8_t* rows, size_t env_bytes, uint32_t blk,
+                                           uint32_t lane, uint32_t n, bool aligned) {
 #pragma unroll
-          for (int q = 0; q < nb; ++q) dst[b0 + q] = (uint8_t)(word >> (8 * q));
-        }
-      }
-      word = 0;
-    }
-  } else {
-    word |= shade << (8u * (ox & 3));
-    if constexpr ((ox & 3) == 3) {
-      if (live) {
-        if (aligned) {
-          *reinterpret_cast<uint32_t*>(dst + (ox & ~3)) = word;
-        } else {
+  for (int i = 0; i < W; ++i) {
+    const uint32_t d = (uint32_t)i * kEnvBlock + lane;
+    const uint32_t env = d / W, w = d % W;
+    const uint32_t v = stage[w * kEnvBlock + (env ^ w)];
+    if (blk * kEnvBlock + env < n) {
+      uint8_t* p = rows + env * env_bytes + 4u * w;
+      if (aligned) {
+        *reinterpret_cast<uint32_t*>(p) = v;
+      } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) dst[(ox & ~3) + q] = (uint8_t)(word >> (8 * q));
-        }
+        for (int q = 0; q < 4; ++q) p[q] = (uint8_t)(v >> (8 * q));
       }
-      word = 0;
     }
   }
-}
-
-template <int... ox>
-__device__ __forceinline__ void render_row(std::integer_sequence<int, ox...>, const uint32_t (&wb)[kTileSlots],
-                                           const uint32_t (&ww)[kTileSlots], uint32_t lcdc, uint32_t scx,
-                                           uint32_t sw, bool win, int wx7, uint32_t bgp, uint32_t obp0,
-                                           uint32_t obp1, bool sprites, const uint16_t (&line)[kDsW][kEnvBlock],
-                                           uint32_t lane, uint8_t* dst, bool aligned, bool live, int packed) {
-  uint32_t word = 0;
-  (render_sample<ox>(wb, ww, lcdc, scx, sw, win, wx7, bgp, obp0, obp1, sprites, line, lane, word, dst, aligned,
-                     live, packed),
-   ...);
 }
 
 // One workgroup per 64-env memory block and 4 output rows; lanes are the
@@ -173,21 +133,22 @@ __device__ __forceinline__ void render_row(std::integer_sequence<int, ox...>, co
 // keeps the opaque sprite pixel with the lowest x (ties: the lower OAM index,
 // the earlier entry), as the reference's per-sample search over OAM selects
 // it.  The BG and window tile rows are fetched for all 21 tile columns at
-// once, then the 80 samples are shaded from registers.
+// once; the samples are then shaded four at a time, one per byte: the
+// group's colours are a byte window of the layer's colour stream, the window
+// layer is blended in by a byte mask, BGP maps colours to shades through a
+// byte permute, and the sprite overlay is a byte mask.
 __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
                                                                 int packed) {
   // OAM entry k of each env: y | x << 8 | tile << 16 | attr << 24
   __shared__ uint32_t oam[40][kEnvBlock];
-  // sprite line buffer per row: 0 = no sprite pixel, else bit 15 set, [0:7]
-  // the sprite's OAM x (its left edge + 8), [8:9] colour, [10] OBP1, [11]
-  // behind non-zero BG
-  __shared__ uint16_t obj[kRenderRows][kDsW][kEnvBlock];
+  // sprite line buffer per row, 4 samples per (group, lane): 0 = no sprite
+  // pixel, else bits [0:1] its shade (palette applied), [2] behind non-zero
+  // BG, [3] set, [8:15] the sprite's OAM x (its left edge + 8)
+  __shared__ __align__(16) uint16_t obj[kRenderRows][kGroups][kEnvBlock][4];
   const uint32_t lane = threadIdx.x & (kEnvBlock - 1);
   const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> kEnvBlockShift);
   const uint32_t blk = blockIdx.x;
-  const uint32_t e = blk * kEnvBlock + lane;
-  const bool live = e < (uint32_t)s.n;  // the block's spare lanes render but never store
-  const Row r{s.mem + ((size_t)blk << 22), lane};
+  const Row r{s.mem + ((size_t)blk << 22), lane};  // the block's spare lanes render but never store
 #pragma unroll
   for (int i = 0; i < 40 / kRenderRows; ++i) {
     const uint32_t k = wv + (uint32_t)(kRenderRows * i);
@@ -200,12 +161,11 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
   const uint32_t bgp = r.M(0xFF47), obp0 = r.M(0xFF48), obp1 = r.M(0xFF49);
   const uint32_t wy = r.M(0xFF4A), wx = r.M(0xFF4B);
   const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
-  const bool sprites = (lcdc & 0x02u) != 0u;
-  uint16_t (&line)[kDsW][kEnvBlock] = obj[wv];
-  __syncthreads();
-  if (sprites) {
+  uint16_t (&line)[kGroups][kEnvBlock][4] = obj[wv];
 #pragma unroll
-    for (int ox = 0; ox < kDsW; ++ox) line[ox][lane] = 0;
+  for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&line[g][lane][0]) = make_uint2(0u, 0u);
+  __syncthreads();
+  if (lcdc & 0x02u) {
     uint32_t on_line = 0;
     for (uint32_t k = 0; k < 40u && on_line < 10u; ++k) {
       const uint32_t ent = oam[k][lane];
@@ -227,7 +187,8 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
       }
       const uint32_t ta = 0x8000u + tile * 16u + row * 2u;
       const uint32_t lo = r.M(ta), hi = r.M(ta + 1u);
-      const uint32_t tag = 0x8000u | sx | (((attr >> 4) & 1u) << 10) | (((attr >> 7) & 1u) << 11);
+      const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
+      const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
       const int left = (int)sx - 8;
       // the sampled columns x = 2*ox inside [left, left + 8)
       for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
@@ -236,29 +197,74 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
         const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
         const uint32_t color = (((hi >> bit) & 1u) << 1) | ((lo >> bit) & 1u);
         if (color == 0) continue;
-        const uint32_t cur = line[x >> 1][lane];
-        if (cur == 0 || sx < (cur & 0xFFu)) line[x >> 1][lane] = (uint16_t)(tag | (color << 8));
+        const uint32_t ox = (uint32_t)x >> 1;
+        uint16_t& slot = line[ox >> 2][lane][ox & 3u];
+        const uint32_t cur = slot;
+        if (cur == 0 || sx < (cur >> 8)) slot = (uint16_t)(tag | ((pal >> (color * 2u)) & 3u));
       }
     }
   }
+
+  const uint32_t bg_on = (lcdc & 0x01u) ? ~0u : 0u;
   const bool win = (lcdc & 0x20u) && y >= wy;
   const int wx7 = (int)wx - 7;
   const uint32_t sw = (7u - wx) & 0xFFu;  // window: px = (x - (WX - 7)) & 0xFF
-  uint32_t wb[kTileSlots], ww[kTileSlots];
+  uint32_t cb[kTileSlots], cw[kTileSlots];
 #pragma unroll
-  for (int j = 0; j < kTileSlots; ++j) wb[j] = ww[j] = 0;
-  if (lcdc & 0x01u) {
+  for (int j = 0; j < kTileSlots; ++j) cb[j] = cw[j] = 0;
+  if (bg_on) {
     // the background unless the window covers the whole row
     if (!(win && wx7 <= 0))
-      load_layer(r, lcdc, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, (y + scy) & 0xFFu, wb);
+      load_layer(r, lcdc, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, (y + scy) & 0xFFu, cb);
     if (win && wx7 < 2 * kDsW - 1)
-      load_layer(r, lcdc, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, (y - wy) & 0xFFu, ww);
+      load_layer(r, lcdc, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, (y - wy) & 0xFFu, cw);
   }
-  uint8_t* dst = out + base + (size_t)e * (packed ? (size_t)kDsWB * kDsH : (size_t)kDsW * kDsH) +
-                 (size_t)oy * (packed ? kDsWB : kDsW);
-  const bool aligned = (((uintptr_t)dst) & 3u) == 0;
-  render_row(std::make_integer_sequence<int, kDsW>{}, wb, ww, lcdc, scx, sw, win, wx7, bgp, obp0, obp1, sprites,
-             line, lane, dst, aligned, live, packed);
+  const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
+  // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
+  const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
+                        (((bgp >> 6) & 3u) << 24)) & bg_on;
+  // Output words are staged over the wavefront's own line buffer: word g of
+  // lane l goes to dword g*64 + (l ^ g), inside the first 256 bytes of group
+  // g/2's entries, which every lane has read by then; the XOR spreads the
+  // column reads of the store phase over the banks.
+  uint32_t* stage = reinterpret_cast<uint32_t*>(&line[0][0][0]);
+  uint32_t pword = 0;
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) {
+    // colours of samples 4g..4g+3, one per byte
+    uint32_t col = __builtin_amdgcn_alignbyte(cb[g + 1], cb[g], qb);
+    if (win) {
+      // samples x = 8g + 2i >= WX - 7 show the window
+      const int d = min(max((wx7 + 1 - 8 * g) >> 1, 0), 4);
+      const uint32_t m = d >= 4 ? 0u : (~0u << (8 * d));
+      col = (col & ~m) | (__builtin_amdgcn_alignbyte(cw[g + 1], cw[g], qw) & m);
+    }
+    col &= bg_on;
+    uint32_t shade = __builtin_amdgcn_perm(0u, pbg, col);
+    const uint2 ob = *reinterpret_cast<const uint2*>(&line[g][lane][0]);
+    const uint32_t w = __builtin_amdgcn_perm(ob.y, ob.x, 0x06040200u);  // low byte of each entry
+    const uint32_t nz = (col | (col >> 1)) & 0x01010101u;
+    const uint32_t show = (w >> 3) & ~((w >> 2) & nz) & 0x01010101u;
+    const uint32_t sm = (show << 8) - show;
+    shade = (sm & w & 0x03030303u) | (~sm & shade);
+    if (packed) {
+      // shades s0..s3 to s0 | s1 << 2 | s2 << 4 | s3 << 6 (no overlapping terms)
+      pword |= ((shade * 0x01041040u) >> 24) << (8 * (g & 3));
+      if ((g & 3) == 3) {
+        stage[(g >> 2) * kEnvBlock + (lane ^ (uint32_t)(g >> 2))] = pword;
+        pword = 0;
+      }
+    } else {
+      stage[g * kEnvBlock + (lane ^ (uint32_t)g)] = shade;
+    }
+  }
+  __syncthreads();
+  uint8_t* rows = out + base + ((size_t)blk * kEnvBlock * kDsH + oy) * (packed ? kDsWB : kDsW);
+  const bool aligned = (((uintptr_t)(out + base)) & 3u) == 0;
+  if (packed)
+    store_rows<kDsWB / 4>(stage, rows, (size_t)kDsWB * kDsH, blk, lane, (uint32_t)s.n, aligned);
+  else
+    store_rows<kDsW / 4>(stage, rows, (size_t)kDsW * kDsH, blk, lane, (uint32_t)s.n, aligned);
 }
 
 // ---------------------------------------------------------------------------
