@@ -381,10 +381,14 @@ __global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int wi
 
 // Masked restore of the interleaved images (mem + cart RAM).  One wavefront
 // per (64-env block, chunk of address rows): the lanes run over the chunk's
-// rows, each reads the row's snapshot byte once, and one store per masked
-// env of the block writes that env's byte in 64 rows.  Blocks without a
-// masked env leave at once.
+// rows.  A masked env's byte shares its 64-byte row with the other 63 envs
+// of the block, so restoring it costs a read and a write-back of the row;
+// each lane therefore reads the env's current bytes first (8 rows at a time,
+// loads ahead of any store) and stores only the bytes that differ from the
+// snapshot, so rows that already hold the snapshot byte are never written.
+// Blocks without a masked env leave at once.
 constexpr uint32_t kResetRows = 4096;
+constexpr int kResetBatch = 8;
 __global__ __launch_bounds__(kEnvBlock) void masked_mem_kernel(DevState s, const uint8_t* snap_mem,
                                                                const uint8_t* snap_cram,
                                                                const uint8_t* mask) {
@@ -393,14 +397,29 @@ __global__ __launch_bounds__(kEnvBlock) void masked_mem_kernel(DevState s, const
   const uint64_t bits = __ballot(e < (uint32_t)s.n && mask[e] != 0);
   if (bits == 0) return;
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
+  const uint32_t a0 = blockIdx.y * kResetRows + l;
   const uint32_t a1 = min(per_env, (blockIdx.y + 1u) * kResetRows);
-  for (uint32_t a = blockIdx.y * kResetRows + l; a < a1; a += kEnvBlock) {
-    const bool in_mem = a < (uint32_t)kMemSize;
-    const uint32_t off = a - (uint32_t)kMemSize;
-    const uint8_t v = in_mem ? snap_mem[a] : snap_cram[off];
-    uint8_t* row = in_mem ? s.mem + mem_index(b << kEnvBlockShift, a)
-                          : s.cram + cram_index(b << kEnvBlockShift, off, (uint32_t)s.cram_stride);
-    for (uint64_t q = bits; q; q &= q - 1) row[__builtin_ctzll(q)] = v;
+  for (uint64_t qb = bits; qb; qb &= qb - 1) {
+    const uint32_t q = (uint32_t)__builtin_ctzll(qb);
+    for (uint32_t a = a0; a < a1; a += kEnvBlock * kResetBatch) {
+      uint8_t* p[kResetBatch];
+      uint32_t want[kResetBatch], cur[kResetBatch];
+#pragma unroll
+      for (int i = 0; i < kResetBatch; ++i) {
+        const uint32_t ai = a + (uint32_t)i * kEnvBlock;
+        const bool ok = ai < a1;
+        const bool in_mem = ai < (uint32_t)kMemSize;
+        const uint32_t off = ai - (uint32_t)kMemSize;
+        p[i] = !ok ? nullptr
+                   : in_mem ? s.mem + mem_index((b << kEnvBlockShift) | q, ai)
+                            : s.cram + cram_index((b << kEnvBlockShift) | q, off, (uint32_t)s.cram_stride);
+        want[i] = !ok ? 0u : in_mem ? snap_mem[ai] : snap_cram[off];
+        cur[i] = ok ? *p[i] : 0u;
+      }
+#pragma unroll
+      for (int i = 0; i < kResetBatch; ++i)
+        if (p[i] != nullptr && cur[i] != want[i]) *p[i] = (uint8_t)want[i];
+    }
   }
 }
 
