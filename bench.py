@@ -44,6 +44,8 @@ def parse_args():
     ap.add_argument("--workload", default="c2", help="c1, c2, c3, c4, c4m3, c5")
     ap.add_argument("--envs", type=int, default=None, help="override the env count")
     ap.add_argument("--frameskip", type=int, default=None, help="override the frameskip")
+    ap.add_argument("--reset-prob", type=float, default=None,
+                    help="override the per-step masked-reset probability")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -100,13 +102,14 @@ def main() -> int:
     from gbxcule_amd.reset_cache import ResetCache
 
     wl = WORKLOADS[args.workload]
-    if args.envs or args.frameskip:
+    if args.envs or args.frameskip or args.reset_prob is not None:
         from dataclasses import replace
 
         wl = replace(
             wl,
             num_envs=args.envs or wl.num_envs,
             frames_per_step=args.frameskip or wl.frames_per_step,
+            reset_prob=wl.reset_prob if args.reset_prob is None else args.reset_prob,
         )
     n, fs = wl.num_envs, wl.frames_per_step
     steps = args.steps if args.steps is not None else (20 if n <= 20000 else 10)

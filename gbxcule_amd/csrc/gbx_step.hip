@@ -723,16 +723,34 @@ struct Lane {
   // cycles) that can be taken in one step from the LDH that just read ly:
   // 0 unless the jump back is taken.  The reference runs the loop one
   // instruction at a time with the timer, PPU, interrupt check and frame
-  // count after each; nothing it observes changes before the next scanline
-  // (LY), TIMA overflow, frame end or interrupt service, so passes are taken
-  // up to the nearest of those, the last one ending at or before it.
-  __device__ int poll_passes(uint32_t dw, uint32_t ly, int cframe) const {
+  // count after each.  The loop observes only the LY it reads, so the passes
+  // run through scanline changes up to the first line whose value ends the
+  // loop, and otherwise to the same horizon as a block copy: the frame end, a
+  // TIMA overflow, a line change that raises a request that would be
+  // serviced, or with the HBlank STAT source on the next mode boundary.  The
+  // last pass ends at or before it.  A pass reads the line at its own start:
+  // the one read now until the next change, then ly + 1, ly + 2, ...
+  __device__ int poll_passes(uint32_t dw, uint32_t ly_read, int cframe) const {
     const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
     // cc: 0 NZ, 1 Z, 2 NC, 3 C
-    const bool flag = (cc & 2u) ? ly < d8 : ly == d8;
+    const bool flag = (cc & 2u) ? ly_read < d8 : ly_read == d8;
     const bool back = flag == ((cc & 1u) != 0u);
     if ((!back) | ff_blocked()) return 0;
-    return ff_horizon(cframe, true, 0u) / 32;
+    if (!(lcdc & 0x80u)) return ff_horizon(cframe, true, 0u) / 32;  // LY stays 0
+    int k = ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u) / 32;
+    // m = line changes ahead to the first line whose value ends the loop
+    // (0: none does)
+    const uint32_t nl = (uint32_t)kLinesPerFrame;
+    const uint32_t v1 = (ly + 1u) % nl;
+    uint32_t m = 1u;  // Z: the first change (conservative: stopping early is exact)
+    if (cc == 0u) m = d8 < nl ? (d8 + nl - ly - 1u) % nl + 1u : 0u;   // NZ: until LY == d8
+    if (cc == 2u) m = d8 == 0u ? 0u : v1 < d8 ? 1u : nl - ly;         // NC: until LY < d8
+    if (cc == 3u) m = d8 >= nl ? 0u : v1 >= d8 ? 1u : (d8 + nl - ly) % nl;  // C: until LY >= d8
+    if (m != 0u) {
+      const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
+      k = min(k, (c + 31) / 32);
+    }
+    return k;
   }
   // End of the plain RAM window holding x (video RAM, work RAM), else 0.
   __device__ static uint32_t ram_window_end(uint32_t x) {
@@ -1037,10 +1055,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           // LDH included) in one step.
           const int k = L.poll_passes(rec.w[15], in.rd0, cframe);
           if (k > 0) {
-            const uint32_t ly = in.rd0, d8 = rec.w[15] & 0xFFu;
+            // A and F as the last pass's LDH and CP leave them
+            const uint32_t off = L.scan + 32u * (uint32_t)(k - 1);
+            const uint32_t ly = ((off < (uint32_t)kCyclesPerLine) | ((L.lcdc & 0x80u) == 0u))
+                                    ? in.rd0
+                                    : (L.ly + off / (uint32_t)kCyclesPerLine) % (uint32_t)kLinesPerFrame;
+            const uint32_t d8 = rec.w[15] & 0xFFu;
             const uint32_t f = ((ly == d8) ? 0x80u : 0u) | 0x40u | (((ly & 15u) < (d8 & 15u)) ? 0x20u : 0u) |
                                ((ly < d8) ? 0x10u : 0u);
-            L.w1 = (L.w1 & 0xFFFF00FFu) | (f << 8);
+            L.w1 = (L.w1 & 0xFFFF0000u) | (f << 8) | ly;
             npc = pc;
             cycles = 32 * k;
             ninstr += 3u * (uint32_t)k - 1u;
