@@ -15,6 +15,12 @@ struct gbx_ctx {
   DevState s{};
   SnapState snap{};
   bool snap_valid = false;
+  // Set once anything but the power-on fill may have written a memory row
+  // below 0x8000 (an import there, or the raw memory pointer handed out).
+  // The step never stores there (ROM-window writes go to the MBC), so while
+  // it is clear every env and the snapshot hold the power-on rows and a
+  // masked restore skips them.
+  bool low_rows_dirty = false;
   uint64_t* hash_k = nullptr;
   int dbg[4] = {0, 0, 0, 0};
 };
@@ -317,7 +323,8 @@ int gbx_masked_reset(gbx_ctx* ctx, const uint8_t* mask_dev, void* stream) {
   CHECK_CTX(ctx);
   if (!ctx->snap_valid) return fail(GBX_E_STATE, "no snapshot: call gbx_snapshot first");
   if (!mask_dev) return fail(GBX_E_INVALID, "mask is NULL");
-  HIP_TRY(launch_masked_reset(ctx->s, ctx->snap, mask_dev, (hipStream_t)stream));
+  HIP_TRY(launch_masked_reset(ctx->s, ctx->snap, mask_dev, ctx->low_rows_dirty ? 0 : 0x8000,
+                              (hipStream_t)stream));
   return GBX_OK;
 }
 
@@ -410,6 +417,7 @@ int gbx_import_mem(gbx_ctx* ctx, int32_t env, int32_t addr, const uint8_t* host_
   if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
   if (addr < 0 || len < 0 || addr + len > kMemSize)
     return fail(GBX_E_INVALID, "write out of range");
+  if (addr < 0x8000 && len > 0) ctx->low_rows_dirty = true;
   if (len == 0) return GBX_OK;
   uint8_t* tmp = nullptr;
   HIP_TRY(hipDeviceSynchronize());
@@ -510,6 +518,7 @@ int gbx_import_env(gbx_ctx* ctx, int32_t env, const int64_t* scalars, const int3
   CHECK_CTX(ctx);
   if (!scalars || !cart_state || !mem) return fail(GBX_E_INVALID, "in is NULL");
   if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
+  ctx->low_rows_dirty = true;  // a full 64 KiB image
   const DevState& s = ctx->s;
   const size_t nb = img_bytes(s.ram_bytes);
   std::vector<uint8_t> h(nb, 0);
@@ -541,7 +550,11 @@ int gbx_buffer(gbx_ctx* ctx, int32_t which, void** dev_ptr, int64_t* nbytes) {
   if (!dev_ptr || !nbytes) return fail(GBX_E_INVALID, "out is NULL");
   const DevState& s = ctx->s;
   switch (which) {
-    case GBX_BUF_MEM: *dev_ptr = s.mem; *nbytes = (int64_t)s.npad * kMemSize; break;
+    case GBX_BUF_MEM:  // the caller may write any row through it
+      *dev_ptr = s.mem;
+      *nbytes = (int64_t)s.npad * kMemSize;
+      ctx->low_rows_dirty = true;
+      break;
     case GBX_BUF_PIX: *dev_ptr = s.pix; *nbytes = (int64_t)s.n * kDsW * kDsH; break;
     case GBX_BUF_PIX_PACKED: *dev_ptr = s.pix_packed; *nbytes = (int64_t)s.n * kDsWB * kDsH; break;
     case GBX_BUF_FRAME_BG: *dev_ptr = s.frame_bg; *nbytes = (int64_t)kScreenW * kScreenH; break;

@@ -386,19 +386,20 @@ __global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int wi
 // each lane therefore reads the env's current bytes first (8 rows at a time,
 // loads ahead of any store) and stores only the bytes that differ from the
 // snapshot, so rows that already hold the snapshot byte are never written.
-// Blocks without a masked env leave at once.
+// Rows below first_row are not restored (the caller knows they already
+// match).  Blocks without a masked env leave at once.
 constexpr uint32_t kResetRows = 4096;
 constexpr int kResetBatch = 8;
 __global__ __launch_bounds__(kEnvBlock) void masked_mem_kernel(DevState s, const uint8_t* snap_mem,
                                                                const uint8_t* snap_cram,
-                                                               const uint8_t* mask) {
+                                                               const uint8_t* mask, uint32_t first_row) {
   const uint32_t b = blockIdx.x, l = threadIdx.x;
   const uint32_t e = (b << kEnvBlockShift) | l;
   const uint64_t bits = __ballot(e < (uint32_t)s.n && mask[e] != 0);
   if (bits == 0) return;
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t a0 = blockIdx.y * kResetRows + l;
-  const uint32_t a1 = min(per_env, (blockIdx.y + 1u) * kResetRows);
+  const uint32_t a0 = first_row + blockIdx.y * kResetRows + l;
+  const uint32_t a1 = min(per_env, first_row + (blockIdx.y + 1u) * kResetRows);
   for (uint64_t qb = bits; qb; qb &= qb - 1) {
     const uint32_t q = (uint32_t)__builtin_ctzll(qb);
     for (uint32_t a = a0; a < a1; a += kEnvBlock * kResetBatch) {
@@ -574,12 +575,12 @@ hipError_t launch_snapshot(const DevState& s, const SnapState& snap, int env, in
 }
 
 hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const uint8_t* mask,
-                               hipStream_t st) {
+                               int first_row, hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t chunks = (per_env + kResetRows - 1) / kResetRows;
+  const uint32_t chunks = (per_env - (uint32_t)first_row + kResetRows - 1) / kResetRows;
   hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + kEnvBlock - 1) / kEnvBlock), chunks),
-                     dim3(kEnvBlock), 0, st, s, snap.mem, snap.cram, mask);
+                     dim3(kEnvBlock), 0, st, s, snap.mem, snap.cram, mask, (uint32_t)first_row);
   hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)s.n), dim3(256), 0, st, s, snap, mask,
                      snap.has_pix);
   return hipGetLastError();

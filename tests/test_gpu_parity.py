@@ -127,3 +127,35 @@ def test_masked_reset_and_senses_parity(carts, bootstub, cart, n):
     finally:
         dut.close()
         ref.close()
+
+
+@pytest.mark.parametrize("route", ["write_memory", "memory_torch"])
+def test_masked_reset_restores_rows_below_0x8000(carts, bootstub, route):
+    """Rows below 0x8000 are skipped by the restore only while nothing but the
+    power-on fill has written them; a write there (an import, or through the
+    raw memory view) must make the next restore put them back."""
+    require_gpu()
+    import torch
+
+    from gbxcule_amd.reset_cache import ResetCache
+
+    n = 64
+    dut = _backend(carts["c3"], bootstub, n, 4, None)
+    try:
+        dut.reset(seed=0)
+        dut.step(seeded_actions(0, 0, n))
+        cache = ResetCache.from_backend(dut, env_idx=0)
+        want = dut.export_memory(0, 1)[0]
+        if route == "write_memory":
+            dut.write_memory(5, 0x1234, b"\xab\xcd")
+        else:
+            dut.memory_torch()[0, 0x1234, 5] = 0xAB
+            torch.cuda.synchronize()
+        assert dut.export_memory(5, 6, 0x1234, 0x1235)[0, 0] == 0xAB
+        mask = np.zeros(n, dtype=np.uint8)
+        mask[5] = 1
+        cache.apply_mask_torch(torch.from_numpy(mask).cuda().bool())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(dut.export_memory(5, 6)[0], want)
+    finally:
+        dut.close()
