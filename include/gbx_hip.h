@@ -54,7 +54,8 @@ enum { GBX_STAGE_EMULATE_ONLY = 0, GBX_STAGE_REWARD_ONLY = 1,
 
 /* Buffers exposed for zero-copy views (gbx_buffer). */
 enum {
-  GBX_BUF_MEM = 0,        /* u8, 64-env blocks: [(N+63)/64][65536][64] */
+  GBX_BUF_MEM = 0,        /* u8, 64-env blocks: [(N+63)/64][65536][64]; once handed out,
+                            gbx_masked_reset also restores rows below 0x8000 */
   GBX_BUF_PIX = 1,        /* u8 [N][72][80] unpacked 2-bit shades */
   GBX_BUF_PIX_PACKED = 2, /* u8 [N][72][20] packed, 4 shades per byte */
   GBX_BUF_OBS = 3,        /* f32 [N][obs_dim] */
