@@ -53,6 +53,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gbx_snapshot": (ctypes.c_int, [_vp, _i32, _i32, _vp]),
     "gbx_masked_reset": (ctypes.c_int, [_vp, _vp, _vp]),
     "gbx_gather_mem": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp]),
+    "gbx_read_mem": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "gbx_write_mem": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "gbx_state_hash": (ctypes.c_int, [_vp, _vp, _vp]),
     "gbx_export_scalar": (ctypes.c_int, [_vp, _i32, _vp]),
     "gbx_import_scalar": (ctypes.c_int, [_vp, _i32, _vp]),

@@ -6,11 +6,12 @@ same constructor keywords, method names, shapes, dtypes and exception types.
 Every launch goes through the C ABI of ``libgbx_hip.so`` on torch's current
 HIP stream; there is no CPU fallback.
 
-Layout difference callers can see: emulated memory is interleaved in blocks of
-64 envs on the device, so ``memory_torch()`` returns the native
-``[blocks, 65536, 64]`` view (env ``e`` is ``[e // 64, :, e % 64]``) instead of
-``[N, 65536]``; ``read_memory_torch`` and ``ram_senses_torch`` give per-env and
-per-address access without copies of the whole image.
+Emulated memory is interleaved in blocks of 64 envs on the device.
+``memory_torch()`` still answers as the reference's env-major ``[N, 65536]``
+uint8 tensor (``EnvMemoryView``: indexing reads and writes the selected
+rectangle in one launch); ``memory_blocks_torch()`` is the native zero-copy
+``[blocks, 65536, 64]`` view, and ``ram_senses_torch`` gathers fixed RAM bytes
+of every env in one launch.
 """
 
 from __future__ import annotations
@@ -336,10 +337,10 @@ class HipVecBackend:
 
     def _apply_lcdc_override(self) -> None:
         """Set LCDC bit 7 where it is clear, keeping the other bits
-        (reference warp_vec.py:734-757)."""
+        (reference warp_vec.py:734-757): one read and one write launch of
+        row 0xFF40."""
         mem = self.memory_torch()
-        col = mem[:, 0xFF40, :]
-        col |= 0x80
+        mem[:, 0xFF40] |= 0x80
 
     def render_pixels_snapshot(self) -> None:
         if not self._initialized:
@@ -426,19 +427,61 @@ class HipVecBackend:
 
     # -- memory ----------------------------------------------------------------
     def memory_torch(self):
-        """Zero-copy ``uint8 [ceil(N/64), 65536, 64]`` view of emulated memory."""
+        """``uint8 [N, 65536]`` emulated memory as the reference's env-major view
+        (warp_vec.py:799-810).  Indexing it (``mem[:, addr]``, ``mem[:, lo:hi]``,
+        ``mem[env, lo:hi]``) returns new tensors of the reference's shapes from
+        one ``gbx_read_mem`` launch; assigning through it writes memory with one
+        ``gbx_write_mem`` launch (see ``gbxcule_amd.memview``)."""
+        if not self._initialized:
+            raise RuntimeError("Backend not initialized. Call reset() first.")
+        v = self._views.get("env_memory")
+        if v is None:
+            from .memview import EnvMemoryView
+
+            torch = _torch()
+            dev = torch.device("cuda", torch.cuda.current_device())
+            v = EnvMemoryView(self.num_envs, dev, self._read_mem_rect, self._write_mem_rect)
+            self._views["env_memory"] = v
+        return v
+
+    def _read_mem_rect(self, env_lo: int, env_hi: int, lo: int, hi: int):
+        torch = _torch()
+        out = torch.empty((env_hi - env_lo, hi - lo), dtype=torch.uint8, device="cuda")
+        if out.numel():
+            self._call(
+                "gbx_read_mem", self.ctx, env_lo, env_hi, lo, hi,
+                ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(_cur_stream()),
+            )  # fmt: skip
+        return out
+
+    def _write_mem_rect(self, env_lo: int, env_hi: int, lo: int, hi: int, src) -> None:
+        torch = _torch()
+        src = src.to(device="cuda", dtype=torch.uint8).contiguous()
+        if tuple(src.shape) != (env_hi - env_lo, hi - lo):
+            raise ValueError("source does not match the memory rectangle")
+        if src.numel():
+            self._call(
+                "gbx_write_mem", self.ctx, env_lo, env_hi, lo, hi,
+                ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(_cur_stream()),
+            )  # fmt: skip
+
+    def memory_blocks_torch(self):
+        """Native zero-copy ``uint8 [ceil(N/64), 65536, 64]`` view: env ``e`` is
+        ``[e // 64, :, e % 64]``.  Once it has been handed out, masked resets
+        also restore rows below 0x8000 (the view can write them)."""
         npad = self._info(_lib.INFO_PADDED_ENVS)
         return self._view(_lib.BUF_MEM, (npad // ENV_BLOCK, MEM_SIZE, ENV_BLOCK), "uint8")
 
     def read_memory_torch(self, env_idx: int, lo: int, hi: int):
-        """Strided zero-copy view of RAM/IO bytes [lo, hi) (lo >= 0x8000) of one env."""
+        """RAM/IO bytes [lo, hi) (lo >= 0x8000) of one env: ``memory_torch()[env_idx,
+        lo:hi]`` as the reference takes it (warp_vec.py:812-822)."""
         if env_idx < 0 or env_idx >= self.num_envs:
             raise ValueError(f"env_idx {env_idx} out of range [0, {self.num_envs})")
         if lo < 0 or hi < 0 or lo > MEM_SIZE or hi > MEM_SIZE or lo > hi:
             raise ValueError(f"Invalid memory range: lo={lo} hi={hi}")
         if lo < ROM_LIMIT:
             raise ValueError("read_memory_torch only supports RAM/IO ranges >= 0x8000")
-        return self.memory_torch()[env_idx // ENV_BLOCK, lo:hi, env_idx % ENV_BLOCK]
+        return self.memory_torch()[env_idx, lo:hi]
 
     def ram_senses_torch(self, addrs, out=None):
         """``out[e, j] = mem[e][addrs[j]]`` for all envs in one launch."""

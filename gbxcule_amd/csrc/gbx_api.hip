@@ -21,6 +21,7 @@ struct gbx_ctx {
   // it is clear every env and the snapshot hold the power-on rows and a
   // masked restore skips them.
   bool low_rows_dirty = false;
+  std::vector<uint8_t> boot_host;  // the power-on fill of rows 0x00-0xFF
   uint64_t* hash_k = nullptr;
   int dbg[4] = {0, 0, 0, 0};
 };
@@ -54,6 +55,17 @@ uint64_t splitmix(uint64_t i) {
 }
 
 constexpr int kHashLen = kMemSize + 128;
+
+// True when bytes [addr, addr + len) of an image differ from the power-on
+// fill (boot image at 0x00-0xFF, zero above) anywhere below 0x8000.
+bool differs_from_fill(const gbx_ctx* c, int32_t addr, const uint8_t* bytes, int32_t len) {
+  for (int32_t i = 0; i < len && addr + i < 0x8000; ++i) {
+    const int32_t a = addr + i;
+    const uint8_t fill = a < 0x100 ? c->boot_host[(size_t)a] : 0;
+    if (bytes[i] != fill) return true;
+  }
+  return false;
+}
 
 void free_ctx(gbx_ctx* c) {
   DevState& s = c->s;
@@ -141,6 +153,14 @@ int choose_step_lanes(int n) {
   return lanes;
 }
 
+// Envs [env_lo, env_hi) x addresses [lo, hi) inside the context.
+int check_rect(const gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo, int32_t hi) {
+  if (env_lo < 0 || env_hi > ctx->s.n || env_lo > env_hi)
+    return fail(GBX_E_INVALID, "env range out of bounds");
+  if (lo < 0 || hi > kMemSize || lo > hi) return fail(GBX_E_INVALID, "address range out of bounds");
+  return GBX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -162,6 +182,7 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   if (rc) return rc;
 
   auto* c = new gbx_ctx();
+  c->boot_host.assign(boot, boot + 0x100);
   DevState& s = c->s;
   s.n = num_envs;
   s.npad = (num_envs + kEnvBlock - 1) & ~(kEnvBlock - 1);
@@ -337,6 +358,30 @@ int gbx_gather_mem(gbx_ctx* ctx, const uint16_t* addrs_dev, int32_t k, uint8_t* 
   return GBX_OK;
 }
 
+int gbx_read_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo, int32_t hi,
+                 uint8_t* out_dev, void* stream) {
+  CHECK_CTX(ctx);
+  if (const int rc = check_rect(ctx, env_lo, env_hi, lo, hi)) return rc;
+  if (env_lo == env_hi || lo == hi) return GBX_OK;
+  if (!out_dev) return fail(GBX_E_INVALID, "out is NULL");
+  HIP_TRY(launch_mem_range(ctx->s, env_lo, env_hi - env_lo, lo, hi - lo, out_dev, 0,
+                           (hipStream_t)stream));
+  return GBX_OK;
+}
+
+int gbx_write_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo, int32_t hi,
+                  const uint8_t* in_dev, void* stream) {
+  CHECK_CTX(ctx);
+  if (const int rc = check_rect(ctx, env_lo, env_hi, lo, hi)) return rc;
+  if (env_lo == env_hi || lo == hi) return GBX_OK;
+  if (!in_dev) return fail(GBX_E_INVALID, "in is NULL");
+  // the bytes are on the device: any write below 0x8000 may change those rows
+  if (lo < 0x8000) ctx->low_rows_dirty = true;
+  HIP_TRY(launch_mem_range(ctx->s, env_lo, env_hi - env_lo, lo, hi - lo,
+                           const_cast<uint8_t*>(in_dev), 1, (hipStream_t)stream));
+  return GBX_OK;
+}
+
 int gbx_state_hash(gbx_ctx* ctx, uint64_t* out_dev, void* stream) {
   CHECK_CTX(ctx);
   if (!out_dev) return fail(GBX_E_INVALID, "out is NULL");
@@ -396,15 +441,13 @@ int gbx_export_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo, int
                    uint8_t* host_out) {
   CHECK_CTX(ctx);
   if (!host_out) return fail(GBX_E_INVALID, "out is NULL");
-  if (env_lo < 0 || env_hi > ctx->s.n || env_lo > env_hi)
-    return fail(GBX_E_INVALID, "env range out of bounds");
-  if (lo < 0 || hi > kMemSize || lo > hi) return fail(GBX_E_INVALID, "address range out of bounds");
+  if (const int rc = check_rect(ctx, env_lo, env_hi, lo, hi)) return rc;
   const size_t total = (size_t)(env_hi - env_lo) * (size_t)(hi - lo);
   if (total == 0) return GBX_OK;
   uint8_t* tmp = nullptr;
   HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMalloc(&tmp, total));
-  hipError_t e = launch_export_mem(ctx->s, env_lo, env_hi - env_lo, lo, hi - lo, tmp, nullptr);
+  hipError_t e = launch_mem_range(ctx->s, env_lo, env_hi - env_lo, lo, hi - lo, tmp, 0, nullptr);
   if (e == hipSuccess) e = hipMemcpy(host_out, tmp, total, hipMemcpyDeviceToHost);
   (void)hipFree(tmp);
   HIP_TRY(e);
@@ -415,15 +458,16 @@ int gbx_import_mem(gbx_ctx* ctx, int32_t env, int32_t addr, const uint8_t* host_
   CHECK_CTX(ctx);
   if (!host_in && len > 0) return fail(GBX_E_INVALID, "in is NULL");
   if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
-  if (addr < 0 || len < 0 || addr + len > kMemSize)
+  // len > kMemSize - addr, not addr + len > kMemSize: the sum can overflow
+  if (addr < 0 || len < 0 || addr > kMemSize || len > kMemSize - addr)
     return fail(GBX_E_INVALID, "write out of range");
-  if (addr < 0x8000 && len > 0) ctx->low_rows_dirty = true;
   if (len == 0) return GBX_OK;
+  if (differs_from_fill(ctx, addr, host_in, len)) ctx->low_rows_dirty = true;
   uint8_t* tmp = nullptr;
   HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMalloc(&tmp, (size_t)len));
   hipError_t e = hipMemcpy(tmp, host_in, (size_t)len, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = launch_import_mem(ctx->s, env, addr, len, tmp, nullptr);
+  if (e == hipSuccess) e = launch_mem_range(ctx->s, env, 1, addr, len, tmp, 1, nullptr);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   (void)hipFree(tmp);
   HIP_TRY(e);
@@ -518,7 +562,8 @@ int gbx_import_env(gbx_ctx* ctx, int32_t env, const int64_t* scalars, const int3
   CHECK_CTX(ctx);
   if (!scalars || !cart_state || !mem) return fail(GBX_E_INVALID, "in is NULL");
   if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
-  ctx->low_rows_dirty = true;  // a full 64 KiB image
+  // rows below 0x8000 that still hold the power-on fill keep the flag clear
+  if (differs_from_fill(ctx, 0, mem, 0x8000)) ctx->low_rows_dirty = true;
   const DevState& s = ctx->s;
   const size_t nb = img_bytes(s.ram_bytes);
   std::vector<uint8_t> h(nb, 0);

@@ -40,10 +40,11 @@ hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const u
 hipError_t launch_gather(const DevState& s, const uint16_t* addrs, int k, uint8_t* out,
                          hipStream_t st);
 hipError_t launch_hash(const DevState& s, const uint64_t* K, uint64_t* out, hipStream_t st);
-hipError_t launch_export_mem(const DevState& s, int env_lo, int count, int lo, int len,
-                             uint8_t* dst, hipStream_t st);
-hipError_t launch_import_mem(const DevState& s, int env, int addr, int len, const uint8_t* src,
-                             hipStream_t st);
+// buf[count][len] env-major <-> memory of envs [env_lo, env_lo + count),
+// addresses [lo, lo + len); to_image = 0 reads the image into buf, 1 writes
+// buf into the image.  The caller checks the ranges.
+hipError_t launch_mem_range(const DevState& s, int env_lo, int count, int lo, int len, uint8_t* buf,
+                            int to_image, hipStream_t st);
 hipError_t launch_export_cram(const DevState& s, int env_lo, int count, uint8_t* dst,
                               hipStream_t st);
 

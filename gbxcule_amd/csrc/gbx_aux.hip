@@ -473,18 +473,44 @@ __global__ void hash_kernel(DevState s, const uint64_t* K, uint64_t* out) {
 }
 
 // Layout converters for the synchronous export/import helpers.
-__global__ void export_mem_kernel(DevState s, uint32_t env_lo, uint32_t count, uint32_t lo,
-                                  uint32_t len, uint8_t* dst) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)count * len) return;
-  const uint32_t ei = (uint32_t)(i / len), a = lo + (uint32_t)(i % len);
-  dst[i] = s.mem[mem_index(env_lo + ei, a)];
-}
-__global__ void import_mem_kernel(DevState s, uint32_t env, uint32_t addr, uint32_t len,
-                                  const uint8_t* src) {
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= len) return;
-  s.mem[mem_index(env, addr + i)] = src[i];
+// Copies between a rectangle of the interleaved image (envs [env_lo, env_lo
+// + count), addresses [lo, lo + len)) and an env-major buffer buf[count][len].
+// One workgroup per tile of 64 envs x 64 addresses, staged in LDS: the image
+// side is read or written one address row (64 neighbouring env bytes) per
+// wavefront instruction and the buffer side one env row of 64 addresses, so
+// both sides stay coalesced.  Rows are padded to 65 bytes so the transposed
+// LDS accesses of a wavefront fall into different banks.
+constexpr int kTile = 64;
+constexpr int kTileThreads = 256;
+__global__ __launch_bounds__(kTileThreads) void mem_range_kernel(DevState s, uint32_t env_lo,
+                                                                 uint32_t count, uint32_t lo,
+                                                                 uint32_t len, uint8_t* buf,
+                                                                 int to_image) {
+  __shared__ uint8_t tile[kTile][kTile + 1];  // [address][env]
+  const uint32_t e0 = blockIdx.x * kTile, a0 = blockIdx.y * kTile, t = threadIdx.x;
+  if (!to_image) {
+    for (uint32_t i = t; i < (uint32_t)(kTile * kTile); i += kTileThreads) {
+      const uint32_t ai = i / kTile, ei = i % kTile;  // lanes run over envs
+      if (a0 + ai < len && e0 + ei < count)
+        tile[ai][ei] = s.mem[mem_index(env_lo + e0 + ei, lo + a0 + ai)];
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < (uint32_t)(kTile * kTile); i += kTileThreads) {
+      const uint32_t ei = i / kTile, ai = i % kTile;  // lanes run over addresses
+      if (a0 + ai < len && e0 + ei < count) buf[(size_t)(e0 + ei) * len + a0 + ai] = tile[ai][ei];
+    }
+  } else {
+    for (uint32_t i = t; i < (uint32_t)(kTile * kTile); i += kTileThreads) {
+      const uint32_t ei = i / kTile, ai = i % kTile;
+      if (a0 + ai < len && e0 + ei < count) tile[ai][ei] = buf[(size_t)(e0 + ei) * len + a0 + ai];
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < (uint32_t)(kTile * kTile); i += kTileThreads) {
+      const uint32_t ai = i / kTile, ei = i % kTile;
+      if (a0 + ai < len && e0 + ei < count)
+        s.mem[mem_index(env_lo + e0 + ei, lo + a0 + ai)] = tile[ai][ei];
+    }
+  }
 }
 __global__ void export_cram_kernel(DevState s, uint32_t env_lo, uint32_t count, uint8_t* dst) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -600,20 +626,14 @@ hipError_t launch_hash(const DevState& s, const uint64_t* K, uint64_t* out, hipS
   return hipGetLastError();
 }
 
-hipError_t launch_export_mem(const DevState& s, int env_lo, int count, int lo, int len,
-                             uint8_t* dst, hipStream_t st) {
-  const size_t total = (size_t)count * (size_t)len;
-  if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(export_mem_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, s,
-                     (uint32_t)env_lo, (uint32_t)count, (uint32_t)lo, (uint32_t)len, dst);
-  return hipGetLastError();
-}
-
-hipError_t launch_import_mem(const DevState& s, int env, int addr, int len, const uint8_t* src,
-                             hipStream_t st) {
-  if (len <= 0) return hipSuccess;
-  hipLaunchKernelGGL(import_mem_kernel, dim3((unsigned)((len + 255) / 256)), dim3(256), 0, st, s,
-                     (uint32_t)env, (uint32_t)addr, (uint32_t)len, src);
+hipError_t launch_mem_range(const DevState& s, int env_lo, int count, int lo, int len, uint8_t* buf,
+                            int to_image, hipStream_t st) {
+  if (count <= 0 || len <= 0) return hipSuccess;
+  // callers have checked env_lo + count <= n and lo + len <= 65536
+  // envs on x (unbounded), address tiles on y (at most 1024)
+  const dim3 grid((unsigned)((count + kTile - 1) / kTile), (unsigned)((len + kTile - 1) / kTile));
+  hipLaunchKernelGGL(mem_range_kernel, grid, dim3(kTileThreads), 0, st, s, (uint32_t)env_lo,
+                     (uint32_t)count, (uint32_t)lo, (uint32_t)len, buf, to_image);
   return hipGetLastError();
 }
 

@@ -745,7 +745,10 @@ struct Lane {
     uint32_t m = 1u;  // Z: the first change (conservative: stopping early is exact)
     if (cc == 0u) m = d8 < nl ? (d8 + nl - ly - 1u) % nl + 1u : 0u;   // NZ: until LY == d8
     if (cc == 2u) m = d8 == 0u ? 0u : v1 < d8 ? 1u : nl - ly;         // NC: until LY < d8
-    if (cc == 3u) m = d8 >= nl ? 0u : v1 >= d8 ? 1u : (d8 + nl - ly) % nl;  // C: until LY >= d8
+    // C: until LY >= d8.  From line 153 the changes run 0, 1, ..., d8, so d8 + 1
+    // of them; (d8 + nl - ly - 1) % nl + 1 counts that and also the case
+    // ly == d8 (a program that wrote FF44 reads a smaller LY): nl changes.
+    if (cc == 3u) m = d8 >= nl ? 0u : v1 >= d8 ? 1u : (d8 + nl - ly - 1u) % nl + 1u;
     if (m != 0u) {
       const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
       k = min(k, (c + 31) / 32);

@@ -55,7 +55,8 @@ enum { GBX_STAGE_EMULATE_ONLY = 0, GBX_STAGE_REWARD_ONLY = 1,
 /* Buffers exposed for zero-copy views (gbx_buffer). */
 enum {
   GBX_BUF_MEM = 0,        /* u8, 64-env blocks: [(N+63)/64][65536][64]; once handed out,
-                            gbx_masked_reset also restores rows below 0x8000 */
+                            gbx_masked_reset also restores rows below 0x8000
+                            (gbx_read_mem / gbx_write_mem reach memory without it) */
   GBX_BUF_PIX = 1,        /* u8 [N][72][80] unpacked 2-bit shades */
   GBX_BUF_PIX_PACKED = 2, /* u8 [N][72][20] packed, 4 shades per byte */
   GBX_BUF_OBS = 3,        /* f32 [N][obs_dim] */
@@ -124,6 +125,23 @@ int gbx_masked_reset(gbx_ctx* ctx, const uint8_t* mask_dev, void* stream);
 int gbx_gather_mem(gbx_ctx* ctx, const uint16_t* addrs_dev, int32_t k,
                    uint8_t* out_dev, void* stream);
 
+/* Device-to-device copy of memory bytes [lo, hi) of envs [env_lo, env_hi)
+ * into out_dev, env-major: out_dev[(env - env_lo) * (hi - lo) + (addr - lo)].
+ * It serves the indexing the reference's callers apply to the env-major
+ * [N, 65536] memory_torch() view (backends/warp_vec.py:799-810), e.g.
+ * mem[:, lo:hi] and mem[:, addr] in rl/pokered_packed_parcel_env.py:
+ * 274-291, 387-391.  Enqueued on the stream; never synchronizes. */
+int gbx_read_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo,
+                 int32_t hi, uint8_t* out_dev, void* stream);
+
+/* The reverse: in_dev (same env-major layout) into the rectangle.  Writes
+ * through the reference's memory_torch() view (mem[:, 0xFF40] |= 0x80,
+ * the LCDC override of backends/warp_vec.py:734-757) land here.  A write
+ * with lo < 0x8000 makes gbx_masked_reset restore rows below 0x8000 from
+ * then on. */
+int gbx_write_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo,
+                  int32_t hi, const uint8_t* in_dev, void* stream);
+
 /* Per-env 64-bit linear hash of mem and registers (no reference
  * counterpart: lets callers compare full state without a readback). */
 int gbx_state_hash(gbx_ctx* ctx, uint64_t* out_dev, void* stream);
@@ -135,6 +153,9 @@ int gbx_export_scalar(gbx_ctx* ctx, int32_t field, int64_t* host_out);
 int gbx_import_scalar(gbx_ctx* ctx, int32_t field, const int64_t* host_in);
 int gbx_export_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo,
                    int32_t hi, uint8_t* host_out);
+/* gbx_import_mem and gbx_import_env write rows below 0x8000 only as data:
+ * while every such row still holds the power-on fill (boot image at
+ * 0x00-0xFF, zero above), gbx_masked_reset keeps skipping them. */
 int gbx_import_mem(gbx_ctx* ctx, int32_t env, int32_t addr,
                    const uint8_t* host_in, int32_t len);
 int gbx_export_cart_state(gbx_ctx* ctx, int32_t* host_out);

@@ -5,17 +5,27 @@
 // the reference repository root).  Nothing here is optimised or shared with
 // the HIP product path; it exists to be obviously the same as the reference.
 //
-// Pinning (what checks this restatement besides the HIP kernel):
-//   - tests/test_oracle_known_answers.py: hand-assembled SM83 programs whose
-//     results follow from the published instruction set (sums, BCD, stack
-//     round trips, JOYP values, timer overflow counts, MBC bank reads);
+// Pinning (what checks this restatement besides the HIP kernel; expected
+// values come from the published SM83/DMG definitions and the reference's
+// stated rules, never from this file):
+//   - tests/test_oracle_known_answers.py: every unprefixed opcode outside the
+//     8-bit ALU block, one instruction from random states, against a model
+//     written from the instruction set (loads, 16-bit INC/DEC, stack byte
+//     order, jump/call/return targets, rotates of A, CPL/SCF/CCF, DI/EI/RETI);
+//     planted mistakes in that model must be caught;
 //   - tests/test_oracle_alu.py: every 8-bit ALU/CB op over all operands
-//     against textbook closed forms (carry/half-carry from bit arithmetic);
-//   - tests/test_oracle_timer_ppu.py: brute-force cycle-by-cycle DIV/TIMA
-//     and LY/STAT/VBlank counts against the event-stepped restatement;
-//   - tests/test_oracle_render_reset.py: the reference's known-answer tests
-//     (all-zero / all-0xFF tiles, sprite priority, reset-mask invariants,
-//     obs_v0 / reward_v0 slots).
+//     against closed forms (carries from the full-width result), DAA as BCD;
+//   - tests/test_oracle_programs.py: the public cycle table for every opcode,
+//     the boot stub's post-boot state, JOYP matrix, timer and LY/STAT/VBlank
+//     against cycle-by-cycle brute force, interrupt counts, HALT/EI quirks,
+//     MBC1/MBC3 banks and RTC seconds, echo RAM, OAM DMA, IF/IE masks, serial;
+//   - tests/test_oracle_timer_ppu.py: STAT requests per frame for all 16
+//     source masks against the closed form of the reference's edge rule,
+//     LCD on/off frame accounting (LDH (40),A minus-4 tail, interrupt
+//     service in the same step, the halted-path variant), obs slots 26-31;
+//   - tests/test_oracle_render_reset.py: the reference's renderer known
+//     answers, hand-built scenes, an independent numpy renderer, the obs/
+//     reward stage known answers and the reset-cache invariants.
 #include "gbx_ref.h"
 
 #include <stdlib.h>
@@ -175,22 +185,50 @@ int clamp_bank(int bank, int count, int mask) {
 
 // One env's view of the machine during one cpu_step launch
 // (kernels/cpu_step_builder.py:875-1781).
+//
+// During a launch the env's scalar fields, cart state and per-env byte
+// counters live in this object (on the stepping thread's stack) and are
+// written back at the end: neighbouring envs' fields share cache lines in
+// the machine's env-major arrays, and threads stepping neighbours would
+// otherwise contend for those lines on every instruction.
 struct Env {
   RefMachine& m;
   int i;
   uint8_t* mem;
-  int32_t* cs;
+  int32_t* cs_out;  // the env's row of the machine's cart_state
   int frames_done = 0;
   int release = 0;
+  int32_t sl[REF_NUM_SCALAR_FIELDS];
+  int32_t cs[CS_STRIDE];
+  int64_t data_bytes = 0;
+  uint8_t stat_prev = 0, joyp_sel = 0, ser_ovf = 0;
 
-  int32_t& S(int f) { return m.s32[f][i]; }
+  Env(RefMachine& machine, int env, uint8_t* env_mem, int32_t* env_cs)
+      : m(machine), i(env), mem(env_mem), cs_out(env_cs) {
+    for (int f = 0; f < REF_NUM_SCALAR_FIELDS; ++f) sl[f] = m.s32[f][i];
+    memcpy(cs, cs_out, sizeof(cs));
+    data_bytes = m.data_bytes[i];
+    stat_prev = m.ppu_stat_prev[i];
+    joyp_sel = m.joyp_select[i];
+    ser_ovf = m.serial_overflow[i];
+  }
+  void store() {
+    for (int f = 0; f < REF_NUM_SCALAR_FIELDS; ++f) m.s32[f][i] = sl[f];
+    memcpy(cs_out, cs, sizeof(cs));
+    m.data_bytes[i] = data_bytes;
+    m.ppu_stat_prev[i] = stat_prev;
+    m.joyp_select[i] = joyp_sel;
+    m.serial_overflow[i] = ser_ovf;
+  }
+
+  int32_t& S(int f) { return sl[f]; }
   uint8_t& M(int addr) { return mem[addr]; }
 
   // ---- bus: kernels/cpu_step_builder.py:538-657 ---------------------------
   int read8(int addr) {
     int a = addr & 0xFFFF;
     if (a >= 0xE000 && a < 0xFE00) a -= 0x2000;
-    if (a >= 0x8000) m.data_bytes[i] += 1;
+    if (a >= 0x8000) data_bytes += 1;
     if (a < BOOTROM_SIZE && cs[CS_BOOTROM_ENABLED] != 0) return m.boot[a];
     if (a < ROM_LIMIT) {
       int kind = cs[CS_MBC_KIND];
@@ -330,11 +368,11 @@ struct Env {
   void write8(int addr, int val) {
     int a = addr & 0xFFFF;
     if (a >= 0xE000 && a < 0xFE00) a -= 0x2000;
-    if (a >= 0x8000) m.data_bytes[i] += 1;
+    if (a >= 0x8000) data_bytes += 1;
     uint8_t v8 = (uint8_t)val;
     if (a == 0xFF00) {
       int sel = v8 & 0x30;
-      m.joyp_select[i] = (uint8_t)sel;
+      joyp_sel = (uint8_t)sel;
       M(0xFF00) = (uint8_t)joyp_read(S(REF_ACTIONS), frames_done, release, sel);
       return;
     }
@@ -349,7 +387,7 @@ struct Env {
           m.serial_buf[(int64_t)i * SERIAL_MAX + idx] = (uint8_t)sb;
           S(REF_SERIAL_LEN) = idx + 1;
         } else {
-          m.serial_overflow[i] = 1;
+          ser_ovf = 1;
         }
         M(a) = (uint8_t)(val & 0x7F);
         M(0xFF0F) = (uint8_t)(M(0xFF0F) | 0x08);
@@ -385,7 +423,7 @@ struct Env {
       M(a) = v8;
       int src = (val & 0xFF) << 8;
       for (int k = 0; k < 160; ++k) M(0xFE00 + k) = M((src + k) & 0xFFFF);
-      m.data_bytes[i] += 320;
+      data_bytes += 320;
       return;
     }
     if (a == 0xFFFF) { M(a) = v8 & 0x1F; return; }
@@ -467,12 +505,12 @@ struct Env {
     int en0 = (keep >> 3) & 1, en1 = (keep >> 4) & 1, en2 = (keep >> 5) & 1,
         enl = (keep >> 6) & 1;
     int c0 = mode == 0, c1 = mode == 1, c2 = mode == 2, cl = coincidence;
-    int prev = m.ppu_stat_prev[i] & 0x0F;
+    int prev = stat_prev & 0x0F;
     int p0 = prev & 1, p1 = (prev >> 1) & 1, p2 = (prev >> 2) & 1, pl = (prev >> 3) & 1;
     bool edge = (en0 && !p0 && c0) || (en1 && !p1 && c1) || (en2 && !p2 && c2) ||
                 (enl && !pl && cl);
     if (edge) M(0xFF0F) = (uint8_t)(M(0xFF0F) | 0x02);
-    m.ppu_stat_prev[i] = (uint8_t)(c0 | (c1 << 1) | (c2 << 2) | (cl << 3));
+    stat_prev = (uint8_t)(c0 | (c1 << 1) | (c2 << 2) | (cl << 3));
   }
   void capture_latches(int ly, int wl) {
     if (i != 0) return;
@@ -491,7 +529,7 @@ struct Env {
       wl = 0;
       M(0xFF44) = 0;
       ppu_update_stat(0, 0);
-      m.ppu_stat_prev[i] = 0;
+      stat_prev = 0;
       return lcdc;
     }
     int total = scan + cycles;
@@ -512,7 +550,7 @@ struct Env {
     int mode = ly >= SCREEN_H ? 1 : scan < 80 ? 2 : scan < 250 ? 3 : 0;
     ppu_update_stat(ly, mode);
     int lyc_eq = ly == M(0xFF45) ? 1 : 0;
-    m.ppu_stat_prev[i] =
+    stat_prev =
         (uint8_t)((mode == 0) | ((mode == 1) << 1) | ((mode == 2) << 2) | (lyc_eq << 3));
     return lcdc;
   }
@@ -1049,7 +1087,7 @@ void Env::run(int frames_to_run, int release_after) {
       M(0xFF44) = 0;
       ppu_update_stat(0, 2);
       int lyc0 = M(0xFF45) == 0 ? 1 : 0;
-      m.ppu_stat_prev[i] = (uint8_t)((1 << 2) | (lyc0 << 3));
+      stat_prev = (uint8_t)((1 << 2) | (lyc0 << 3));
       cframe = 0;
       if (++frames_done >= frames_to_run) break;
       continue;
@@ -1310,8 +1348,9 @@ int ref_step(RefMachine* m, const int32_t* actions, int frames_to_run,
 #pragma omp parallel for schedule(dynamic, 4) num_threads(nthreads)
 #endif
   for (int i = env_lo; i < env_hi; ++i) {
-    Env env{*m, i, &m->mem[(size_t)i * MEM_SIZE], &m->cart_state[(size_t)i * CS_STRIDE]};
+    Env env(*m, i, &m->mem[(size_t)i * MEM_SIZE], &m->cart_state[(size_t)i * CS_STRIDE]);
     env.run(frames_to_run, release_after_frames);
+    env.store();
     if (stage != 0) write_post_step(*m, i, stage);
   }
   return 0;

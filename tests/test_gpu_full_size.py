@@ -260,7 +260,7 @@ def test_full_size_rollout_with_masked_reset(carts, bootstub):
         _check_groups(dig, rep_of, tag)
         # senses of the last step must be the raw bytes of each env's memory
         rows = torch.from_numpy(addrs.astype(np.int64)).cuda()
-        want = dut.memory_torch()[:, rows, :].permute(0, 2, 1).reshape(-1, addrs.size)[:n].cpu().numpy()
+        want = dut.memory_blocks_torch()[:, rows, :].permute(0, 2, 1).reshape(-1, addrs.size)[:n].cpu().numpy()
         np.testing.assert_array_equal(senses[-1], want)
 
         sample = _sample(reps, n)

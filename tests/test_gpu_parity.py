@@ -149,7 +149,7 @@ def test_masked_reset_restores_rows_below_0x8000(carts, bootstub, route):
         if route == "write_memory":
             dut.write_memory(5, 0x1234, b"\xab\xcd")
         else:
-            dut.memory_torch()[0, 0x1234, 5] = 0xAB
+            dut.memory_blocks_torch()[0, 0x1234, 5] = 0xAB
             torch.cuda.synchronize()
         assert dut.export_memory(5, 6, 0x1234, 0x1235)[0, 0] == 0xAB
         mask = np.zeros(n, dtype=np.uint8)

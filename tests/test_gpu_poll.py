@@ -166,3 +166,89 @@ def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat, halt):
     finally:
         dut.close()
         ref.close()
+
+
+def ly_write_cart(seed: int) -> bytes:
+    """IME off; waits for line 153, writes FF44 (LY) with a smaller value and
+    polls with JR C until LY >= 153, then writes a value >= d8 and polls with
+    JR NC until LY < d8.  The written value is what the first pass reads; the
+    next scanline change overwrites it."""
+    rng = np.random.default_rng(seed)
+    rom = bytearray(0x8000)
+    _vectors(rom)
+    a = Asm(origin=PROGRAM_ORIGIN)
+    a.ld_rr_d16("SP", 0xDFF0)
+    a.ld_r_d8("A", 0x91)
+    a.ldh_a8_a(0x40)
+    a.label("loop")
+    a.label("w1")
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", 153)
+    a.jr("w1", "NZ")
+    a.ld_r_d8("B", 20)  # about 330 cycles further into line 153
+    a.label("dl")
+    a.dec_r("B")
+    a.jr("dl", "NZ")
+    a.ld_r_d8("A", int(rng.integers(0, 153)))
+    a.ldh_a8_a(0x44)
+    a.label("w2")  # while LY < 153: from line 153, once around the frame
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", 153)
+    a.jr("w2", "C")
+    d8 = int(rng.integers(1, 150))
+    a.ld_r_d8("A", int(rng.integers(d8, 256)))
+    a.ldh_a8_a(0x44)
+    a.label("w3")  # while LY >= d8
+    a.ldh_a_a8(0x44)
+    a.alu_d8("CP", d8)
+    a.jr("w3", "NC")
+    a.ld_a_a16(0xC000)
+    a.inc_r("A")
+    a.ld_a16_a(0xC000)
+    a.jp("loop")
+    code = a.resolve()
+    rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
+    return finalize_rom(rom, "GBXAMD LYW", 0x00, 0x00, 0x00)
+
+
+@pytest.mark.parametrize("seed", [21, 22])
+def test_poll_after_ly_write_with_frame_offset(bootstub, seed):
+    """A poll that starts on line 153 after the program wrote FF44 runs once
+    around the frame (154 scanline changes).  With the frame count out of
+    step with the scanlines (each env gets a random cycle_in_frame, as a
+    loaded savestate can carry), the frame end does not bound that run, so the
+    loop's own end must.  Half the envs get a frame end just past the change
+    into line 153 (cycle_in_frame ahead of the scanline position by a line
+    less 40-300 cycles): the window where a bound taken from the frame end
+    alone would batch passes that read LY = 153."""
+    require_gpu()
+    from gbxcule_amd.backend import HipVecBackend
+
+    rom = ly_write_cart(seed)
+    n, fs, steps = 128, 6, 5
+    dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
+                        stage="emulate_only", bootrom=bootstub)  # fmt: skip
+    ref = RefMachine(n, rom, bootstub)
+    try:
+        dut.reset(seed=seed)
+        ref.step(None, 0, 0, "emulate_only")
+        act = seeded_actions(seed, 0, n)
+        dut.step(act)
+        ref.step(act, fs, 8, "emulate_only", threads=8)
+        rng = np.random.default_rng(seed)
+        off = rng.integers(0, 70224, n)
+        pos = ref.field("ppu_ly").astype(np.int64) * 456 + ref.field("ppu_scanline_cycle")
+        near = (pos + 456 - rng.integers(40, 300, n)) % 70224
+        off[::2] = near[::2]
+        ref.field("cycle_in_frame")[:] = off
+        dut.import_field("cycle_in_frame", off)
+        for k in range(1, steps):
+            act = seeded_actions(seed, k, n)
+            dut.step(act)
+            ref.step(act, fs, 8, "emulate_only", threads=8)
+            assert_same_state(dut, ref, step=k, tag=f"lyw{seed}")
+        assert int(ref.mem[:, 0xC000].min()) > 0  # every env finished loop passes
+        assert int(ref.field("trap_flag").sum()) == 0
+    finally:
+        dut.close()
+        ref.close()
