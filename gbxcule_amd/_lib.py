@@ -66,6 +66,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "gbx_export_serial": (ctypes.c_int, [_vp, _vp]),
     "gbx_export_latches": (ctypes.c_int, [_vp, _vp]),
     "gbx_export_env": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp]),
+    "gbx_export_env_noalloc": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp]),
     "gbx_import_env": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "gbx_buffer": (ctypes.c_int, [_vp, _i32, ctypes.POINTER(_vp), _P64]),
     "gbx_info": (ctypes.c_int, [_vp, _i32, _P64]),

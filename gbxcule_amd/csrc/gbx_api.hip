@@ -2,6 +2,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -11,8 +12,20 @@
 
 using namespace gbx;
 
+// Static scratch of gbx_export_env_noalloc: one env image (scalars, cart
+// state, 64 KiB of memory, cart RAM, scanline latches) staged between the
+// gather kernel and the copies to the caller's host buffers.  128 KiB holds
+// the image of every cart with at most 32 KiB of cart RAM.  Each GPU the
+// library runs on holds its own copy until the process ends; every call on
+// one GPU reuses it, so calls that overlap on one GPU race.  In host code the
+// name is only a stand-in: kernels get the device address taken once per
+// device with hipGetSymbolAddress (scratch_ptr).
+constexpr size_t kScratchBytes = 128 * 1024;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 struct gbx_ctx {
   DevState s{};
+  int device = 0;  // the device current at gbx_create
   SnapState snap{};
   bool snap_valid = false;
   // Set once anything but the power-on fill may have written a memory row
@@ -55,6 +68,29 @@ uint64_t splitmix(uint64_t i) {
 }
 
 constexpr int kHashLen = kMemSize + 128;
+
+// Device address of `scratch` per device, taken once per device with that
+// device current (gbx_create) and kept for the life of the process.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_setup(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(GBX_E_UNSUPPORTED, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] != nullptr) return GBX_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr)
+    return fail(GBX_E_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  g_scratch_ptr[dev] = p;
+  return GBX_OK;
+}
+
+void* scratch_ptr(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
+}
 
 // True when bytes [addr, addr + len) of an image differ from the power-on
 // fill (boot image at 0x00-0xFF, zero above) anywhere below 0x8000.
@@ -180,9 +216,13 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   int64_t rom_bytes;
   int rc = parse_header(rom, rom_len, &kind, &rom_bytes, &ram_bytes);
   if (rc) return rc;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(GBX_E_HIP, "hipGetDevice failed");
+  if ((rc = scratch_setup(dev)) != GBX_OK) return rc;
 
   auto* c = new gbx_ctx();
   c->boot_host.assign(boot, boot + 0x100);
+  c->device = dev;
   DevState& s = c->s;
   s.n = num_envs;
   s.npad = (num_envs + kEnvBlock - 1) & ~(kEnvBlock - 1);
@@ -554,6 +594,34 @@ int gbx_export_env(gbx_ctx* ctx, int32_t env, int64_t* scalars, int32_t* cart_st
   memcpy(cart_state, h.data() + kImgCart, sizeof(int32_t) * kCartStateStride);
   memcpy(mem, h.data() + kImgMem, kMemSize);
   if (cart_ram && s.ram_bytes > 0) memcpy(cart_ram, h.data() + kImgCram, (size_t)s.ram_bytes);
+  return GBX_OK;
+}
+
+int gbx_export_env_noalloc(gbx_ctx* ctx, int32_t env, int64_t* scalars, int32_t* cart_state,
+                           uint8_t* mem, uint8_t* cart_ram) {
+  CHECK_CTX(ctx);
+  if (!scalars || !cart_state || !mem) return fail(GBX_E_INVALID, "out is NULL");
+  if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
+  const DevState& s = ctx->s;
+  const size_t nb = img_bytes(s.ram_bytes);
+  if (nb > kScratchBytes)
+    return fail(GBX_E_UNSUPPORTED, "env image of " + std::to_string(nb) + " bytes exceeds the " +
+                                       std::to_string(kScratchBytes) +
+                                       "-byte static scratch (cart RAM above 32 KiB); use gbx_export_env");
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev != ctx->device) return fail(GBX_E_STATE, "the context's device is not the current device");
+  uint8_t* img = static_cast<uint8_t*>(scratch_ptr(dev));
+  if (img == nullptr) return fail(GBX_E_STATE, "static scratch not set up on this device");
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(launch_env_image(s, env, img, 0, 0, nullptr));
+  // straight from the scratch into the caller's buffers: no staging copy
+  HIP_TRY(hipMemcpy(scalars, img, sizeof(int64_t) * GBX_NUM_FIELDS, hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(cart_state, img + kImgCart, sizeof(int32_t) * kCartStateStride,
+                    hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(mem, img + kImgMem, kMemSize, hipMemcpyDeviceToHost));
+  if (cart_ram && s.ram_bytes > 0)
+    HIP_TRY(hipMemcpy(cart_ram, img + kImgCram, (size_t)s.ram_bytes, hipMemcpyDeviceToHost));
   return GBX_OK;
 }
 
