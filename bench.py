@@ -6,15 +6,19 @@ gather), on synthetic seeded cartridges with a seeded 8-way action trace that
 is uploaded to the device before timing.  Metric: env-steps/s (whole job) and
 emulated frames/s = env-steps/s * frameskip.
 
-Default workload: 16,384 envs, frameskip 24, CPU-step only (the config the
-headline metric is quoted on).  ``--workload`` selects the others.
+The headline ``value`` is the CPU-step workload at 16,384 envs, frameskip 24
+(``--workload`` selects another).  The same JSON line carries measured
+sub-objects for the 128K-env half of the metric (``workloads``): the banked
+cart with interrupts at 131,072 envs, frameskip 24 and 1, and the RL rollout
+shape at 131,072 envs, each timed the same way in this run.
 
-Prints one JSON line.  ``roofline`` is computed for the step kernel from its
-algorithmic bytes per env-step (922 B of per-env state read+written plus the
-emulated data-memory bytes the oracle counts on the same trace) and its
-average duration measured with HIP events; ``cpu_baseline`` times the oracle
-(a C++ restatement of the reference Warp CPU backend) on a bounded prefix of
-the same workload on the host cores.
+``roofline`` is computed for the step kernel from its algorithmic bytes per
+env-step (922 B of per-env state read+written plus the emulated data-memory
+bytes the oracle counts on the same trace) and its average duration measured
+with HIP events on the stream it is launched on.  ``cpu_baseline`` times the
+oracle (a C++ restatement of the reference Warp CPU backend) on a bounded
+sample of the same workload on the host cores allotted to this process, and
+on one thread.
 """
 
 from __future__ import annotations
@@ -24,6 +28,7 @@ import json
 import os
 import sys
 import time
+from dataclasses import replace
 from pathlib import Path
 
 import numpy as np
@@ -34,6 +39,16 @@ sys.path.insert(0, str(ROOT))
 METRIC = "env-steps/sec @ frameskip 24 (16K & 128K envs); emulated frames/sec"
 STATE_BYTES = 922  # per-env scalar state + FF00-FFFF page, read and written once
 HBM_PEAK_GBS = 8000.0
+# the 128K-env workloads timed beside the headline: (key, workload, envs, frameskip, steps)
+EXTRA = (
+    ("c4_mbc1_irq_131k_fs24", "c4", 131_072, 24, 10),
+    ("c4_mbc1_irq_131k_fs1", "c4", 131_072, 1, 50),
+    ("c5_rl_rollout_131k_fs24", "c5", 131_072, 24, 20),
+)
+TARGETS = {  # env-steps/s the C4 131K target names, per frameskip
+    ("c4", 131_072, 24): 400_000,
+    ("c4", 131_072, 1): 10_000_000,
+}
 
 
 def parse_args():
@@ -48,17 +63,21 @@ def parse_args():
                     help="override the per-step masked-reset probability")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (PMC scaling reference)")
     return ap.parse_args()
 
 
-def cpu_threads() -> int:
+def cpu_threads() -> tuple[int, int]:
+    """(threads to use, CPUs this process may run on).  The pool of the GPU
+    host is shared per GPU; OMP_NUM_THREADS states this process's share."""
     try:
-        n = len(os.sched_getaffinity(0))
+        avail = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        avail = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(avail, share)), avail
 
 
 def oracle_sample(wl, rom, boot, n_env, seconds, threads, max_steps=200):
@@ -85,6 +104,147 @@ def oracle_sample(wl, rom, boot, n_env, seconds, threads, max_steps=200):
     return steps, dt, data_per_env_step, instr_per_env_step
 
 
+def profile_file(key: str, n: int, fs: int):
+    """A committed rocprof summary for this workload shape, if any."""
+    f = ROOT / "profiles" / f"traffic_{key}_{n}{'' if fs == 24 else f'_fs{fs}'}.json"
+    return json.loads(f.read_text()) if f.exists() else None
+
+
+def time_workload(wl, steps: int, warmup: int) -> dict:
+    """Run ``warmup`` + ``steps`` steps of ``wl`` and time the last ``steps``."""
+    import torch
+
+    from gbxcule_amd.backend import HipVecBackend
+    from gbxcule_amd.carts.bootstub import build_bootstub
+    from gbxcule_amd.carts.synth import seeded_actions
+    from gbxcule_amd.reset_cache import ResetCache
+
+    n, fs = wl.num_envs, wl.frames_per_step
+    dev = torch.device("cuda", 0)
+    be = HipVecBackend(
+        wl.rom(),
+        num_envs=n,
+        frames_per_step=fs,
+        release_after_frames=wl.release_after_frames,
+        stage=wl.stage,
+        render_pixels=wl.render == "unpacked",
+        render_pixels_packed=wl.render == "packed",
+        render_on_step=False,
+        bootrom=build_bootstub(),
+    )
+    try:
+        be.reset(seed=wl.actions_seed)
+        total = warmup + steps
+        # timed steps use step indices 0..steps-1 of the seeded trace; warmup
+        # steps draw from indices past 10**6 so they never overlap
+        idx = [10**6 + k for k in range(warmup)] + list(range(steps))
+        trace = np.stack([seeded_actions(wl.actions_seed, k, n) for k in idx]).astype(np.int32)
+        actions = torch.from_numpy(trace).to(dev)
+        masks = cache = senses_out = packed_out = None
+        if wl.reset_prob > 0:
+            rng = np.random.default_rng(wl.actions_seed + 1000)
+            masks = torch.from_numpy((rng.random((total, n)) < wl.reset_prob).astype(np.uint8)).to(dev)
+            cache = ResetCache.from_backend(be, env_idx=0)
+        if wl.senses:
+            rng = np.random.default_rng(wl.actions_seed + 2000)
+            addrs = np.sort(rng.choice(np.arange(0xC000, 0xE000), wl.senses, replace=False))
+            senses_out = torch.empty((n, wl.senses), dtype=torch.uint8, device=dev)
+        if wl.render == "packed":
+            packed_out = torch.empty((n, 72, 20), dtype=torch.uint8, device=dev)
+
+        def one_step(k, ev=None):
+            if ev is not None:
+                ev[0].record()
+            be.step_torch(actions[k])
+            if ev is not None:
+                ev[1].record()
+            if wl.render == "packed":
+                be.render_pixels_snapshot_packed_to_torch(packed_out, 0)
+            elif wl.render == "unpacked":
+                be.render_pixels_snapshot()
+            if cache is not None:
+                cache.apply_mask_torch(masks[k])
+            if senses_out is not None:
+                be.ram_senses_torch(addrs, out=senses_out)
+
+        for k in range(warmup):
+            one_step(k)
+        torch.cuda.synchronize()
+        # the kernel runs on torch's current stream, where these events record
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            one_step(warmup + i, events[i])
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
+        value = n * steps / elapsed
+        return {
+            "value": value,
+            "unit": "env-steps/s",
+            "num_envs": n,
+            "frameskip": fs,
+            "steps": steps,
+            "warmup": warmup,
+            "ms_per_step": elapsed / steps * 1e3,
+            "step_kernel_ms": kernel_ms,
+            "frames_per_sec": value * fs,
+            "emulated_instr_per_sec": float(be.export_field("instr_count").sum()) / total / (elapsed / steps),
+            "traps": int(be.export_field("trap_flag").sum()),
+            "step_lanes": be.step_lanes,
+        }
+    finally:
+        be.close()
+
+
+def roofline(key: str, res: dict, data_b: float, instr_b: float) -> dict:
+    """Step-kernel roofline: algorithmic bytes per launch over its measured
+    duration; rocprof traffic per launch where a committed summary exists."""
+    n, fs, kernel_ms = res["num_envs"], res["frameskip"], res["step_kernel_ms"]
+    bytes_per_env_step = STATE_BYTES + data_b
+    achieved = n * bytes_per_env_step / (kernel_ms * 1e-3) / 1e9
+    prof = profile_file(key, n, fs)
+    out = {
+        "bound": "hbm",
+        "achieved": achieved,
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": achieved / HBM_PEAK_GBS,
+        "traffic": prof.get("bytes_per_launch") if prof else None,
+        "kernel": "gbx::step_kernel",
+        "bytes_per_env_step": bytes_per_env_step,
+        "instr_per_env_step": instr_b,
+        "achieved_counts": "emulated accesses: the step kernel batches poll and copy loops and "
+        "keeps hot registers in VGPRs, so it moves far fewer bytes than it emulates",
+    }
+    if prof:
+        out["traffic_source"] = prof.get("source")
+    return out
+
+
+def valu_object(key: str, res: dict):
+    """VALU issue against the chip's peak: profiled wave-instructions per
+    launch (committed rocprof summary of the same workload) x 64 lanes over
+    this run's measured kernel time, plus the profiled active-lane fraction."""
+    prof = profile_file(key, res["num_envs"], res["frameskip"])
+    if not prof or not prof.get("valu_wave_insts_per_launch"):
+        return None
+    lane_ops = prof["valu_wave_insts_per_launch"] * 64 / (res["step_kernel_ms"] * 1e-3)
+    peak = prof["valu_peak_lane_ops_per_s"]
+    out = {
+        "achieved": lane_ops,
+        "peak": peak,
+        "unit": "lane-op/s (issue slots)",
+        "frac": lane_ops / peak,
+        "source": prof.get("source"),
+    }
+    for k in ("active_lane_frac", "valu_busy", "useful_lane_frac"):
+        if k in prof:
+            out[k] = prof[k]
+    return out
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -96,15 +256,19 @@ def main() -> int:
         return 2
     import torch
 
-    from gbxcule_amd.backend import HipVecBackend
     from gbxcule_amd.carts.bootstub import build_bootstub
-    from gbxcule_amd.carts.synth import WORKLOADS, seeded_actions
-    from gbxcule_amd.reset_cache import ResetCache
+    from gbxcule_amd.carts.synth import WORKLOADS
+
+    torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     wl = WORKLOADS[args.workload]
     if args.envs or args.frameskip or args.reset_prob is not None:
-        from dataclasses import replace
-
         wl = replace(
             wl,
             num_envs=args.envs or wl.num_envs,
@@ -113,131 +277,55 @@ def main() -> int:
         )
     n, fs = wl.num_envs, wl.frames_per_step
     steps = args.steps if args.steps is not None else (20 if n <= 20000 else 10)
-    warmup = args.warmup
+    res = time_workload(wl, steps, args.warmup)
     rom, boot = wl.rom(), build_bootstub()
-    torch.cuda.set_device(0)
-    dev = torch.device("cuda", 0)
 
-    be = HipVecBackend(
-        rom,
-        num_envs=n,
-        frames_per_step=fs,
-        release_after_frames=wl.release_after_frames,
-        stage=wl.stage,
-        render_pixels=wl.render == "unpacked",
-        render_pixels_packed=wl.render == "packed",
-        render_on_step=False,
-        bootrom=boot,
-    )
-    be.reset(seed=wl.actions_seed)
-    total = warmup + steps
-    # timed steps use step indices 0..steps-1 of the seeded trace; warmup
-    # steps draw from indices past 10**6 so they never overlap
-    idx = [10**6 + k for k in range(warmup)] + list(range(steps))
-    trace = np.stack([seeded_actions(wl.actions_seed, k, n) for k in idx]).astype(np.int32)
-    actions = torch.from_numpy(trace).to(dev)
-    masks = None
-    senses_out = None
-    cache = None
-    if wl.reset_prob > 0:
-        rng = np.random.default_rng(wl.actions_seed + 1000)
-        masks = torch.from_numpy((rng.random((total, n)) < wl.reset_prob).astype(np.uint8)).to(dev)
-        cache = ResetCache.from_backend(be, env_idx=0)
-    if wl.senses:
-        rng = np.random.default_rng(wl.actions_seed + 2000)
-        addrs = np.sort(rng.choice(np.arange(0xC000, 0xE000), wl.senses, replace=False))
-        senses_out = torch.empty((n, wl.senses), dtype=torch.uint8, device=dev)
-    packed_out = None
-    if wl.render == "packed":
-        packed_out = torch.empty((n, 72, 20), dtype=torch.uint8, device=dev)
+    # the 128K-env workloads, each timed the same way
+    extra = {}
+    if not args.no_extra:
+        for key, wname, en, efs, esteps in EXTRA:
+            ewl = replace(WORKLOADS[wname], num_envs=en, frames_per_step=efs)
+            r = time_workload(ewl, esteps, args.warmup)
+            _, _, db, ib = oracle_sample(ewl, ewl.rom(), boot, 64, 0.0, cpu_threads()[0], max_steps=1)
+            r["roofline"] = roofline(wname, r, db, ib)
+            r["valu"] = valu_object(wname, r)
+            r["workload"] = ewl.name
+            tgt = TARGETS.get((wname, en, efs))
+            if tgt:
+                r["target"] = tgt
+            extra[key] = r
 
-    def one_step(k, ev=None):
-        if ev is not None:
-            ev[0].record()
-        be.step_torch(actions[k])
-        if ev is not None:
-            ev[1].record()
-        if wl.render == "packed":
-            be.render_pixels_snapshot_packed_to_torch(packed_out, 0)
-        elif wl.render == "unpacked":
-            be.render_pixels_snapshot()
-        if cache is not None:
-            cache.apply_mask_torch(masks[k])
-        if senses_out is not None:
-            be.ram_senses_torch(addrs, out=senses_out)
-
-    if args.copy_calibration:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-
-    for k in range(warmup):
-        one_step(k)
-    torch.cuda.synchronize()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        one_step(warmup + i, events[i])
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    step_ms = [a.elapsed_time(b) for a, b in events]
-    kernel_ms = float(np.mean(step_ms))
-    value = n * steps / elapsed
-    traps = int(be.export_field("trap_flag").sum())
-    lanes = be.step_lanes
-    instr_gpu = float(be.export_field("instr_count").sum())
-
-    # CPU baseline on a bounded prefix of the same trace; also yields the
+    # CPU baseline on a bounded sample of the same trace; also yields the
     # per-env-step emulated data bytes for the roofline.
-    threads = cpu_threads()
+    threads, avail = cpu_threads()
     cpu = None
     if args.no_cpu_baseline:
         _, _, data_b, instr_b = oracle_sample(wl, rom, boot, 64, 0.0, threads, max_steps=1)
     else:
-        n_cpu = min(n, 32 * threads)
-        c_steps, c_dt, data_b, instr_b = oracle_sample(
-            wl, rom, boot, n_cpu, args.cpu_seconds, threads
-        )
+        n_cpu = min(n, 64 * threads)
+        c_steps, c_dt, data_b, instr_b = oracle_sample(wl, rom, boot, n_cpu, args.cpu_seconds, threads)
+        n1 = min(n, 32)
+        s1, dt1, _, _ = oracle_sample(wl, rom, boot, n1, args.cpu_seconds / 2, 1)
         cpu = {
             "value": n_cpu * c_steps / c_dt,
             "unit": "env-steps/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"oracle (C++ restatement of the reference Warp CPU step) on envs "
-            f"0..{n_cpu - 1} of the same cart and action trace, {c_steps} steps of "
-            f"frameskip {fs}, {threads} OpenMP threads, {c_dt:.1f} s",
+            "host_cpus": avail,
+            "single_thread_value": n1 * s1 / dt1,
+            "sample": f"oracle (C++ restatement of the reference Warp CPU step, g++ -O3 "
+            f"-march=x86-64-v3) on envs 0..{n_cpu - 1} of the same cart and action trace, "
+            f"{c_steps} steps of frameskip {fs}, {threads} OpenMP threads ({avail} CPUs "
+            f"available), {c_dt:.1f} s; single thread: envs 0..{n1 - 1}, {s1} steps, {dt1:.1f} s",
         }
-    bytes_per_env_step = STATE_BYTES + data_b
-    achieved = n * bytes_per_env_step / (kernel_ms * 1e-3) / 1e9
-    traffic = None
-    valu = None
-    tfile = ROOT / "profiles" / f"traffic_{args.workload}_{n}.json"
-    if tfile.exists() and fs == WORKLOADS[args.workload].frames_per_step:
-        t = json.loads(tfile.read_text())
-        traffic = t.get("bytes_per_launch")
-        if t.get("valu_wave_insts_per_launch"):
-            # VALU issue slots: profiled wave-instructions per launch x 64 lanes
-            # over this run's measured kernel time
-            lane_ops = t["valu_wave_insts_per_launch"] * 64 / (kernel_ms * 1e-3)
-            peak = t["valu_peak_lane_ops_per_s"]
-            valu = {
-                "achieved": lane_ops,
-                "peak": peak,
-                "unit": "lane-op/s",
-                "frac": lane_ops / peak,
-                "source": t.get("source"),
-            }
     out = {
         "metric": METRIC,
-        "value": value,
+        "value": res["value"],
         "unit": "env-steps/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": elapsed / steps * 1e3,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -255,27 +343,17 @@ def main() -> int:
             "render": wl.render,
             "reset_prob": wl.reset_prob,
             "senses": wl.senses,
-            "step_lanes": lanes,
+            "step_lanes": res["step_lanes"],
         },
-        "frames_per_sec": value * fs,
-        "emulated_instr_per_sec": instr_gpu / max(warmup + steps, 1) / (elapsed / steps),
-        "step_kernel_ms": kernel_ms,
-        "traps": traps,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "kernel": "gbx::step_kernel",
-            "bytes_per_env_step": bytes_per_env_step,
-            "instr_per_env_step": instr_b,
-        },
-        "valu": valu,
+        "frames_per_sec": res["frames_per_sec"],
+        "emulated_instr_per_sec": res["emulated_instr_per_sec"],
+        "step_kernel_ms": res["step_kernel_ms"],
+        "traps": res["traps"],
+        "roofline": roofline(args.workload, res, data_b, instr_b),
+        "valu": valu_object(args.workload, res) if fs == WORKLOADS[args.workload].frames_per_step else None,
         "cpu_baseline": cpu,
+        "workloads": extra,
     }
-    be.close()
     print(json.dumps(out))
     return 0
 

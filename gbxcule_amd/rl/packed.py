@@ -74,20 +74,18 @@ def packed_l1_distance(packed_obs, packed_goal):
     (reference packed_metrics.py:16-41).  Computed with shifts on the packed
     bytes, no table gather; the sums are small integers, exact in float32."""
     torch = _torch()
-    if packed_obs.dtype is not torch.uint8:
-        raise ValueError("packed_obs must be uint8")
-    if packed_goal.dtype is not torch.uint8:
-        raise ValueError("packed_goal must be uint8")
-    if packed_obs.ndim != 4:
-        raise ValueError("packed_obs must be [N, 1, H, W_bytes]")
-    if packed_goal.ndim == 3:
-        packed_goal = packed_goal.unsqueeze(0)
-    if packed_goal.ndim != 4:
-        raise ValueError("packed_goal must be [1, 1, H, W_bytes] or [1, H, W_bytes]")
-    if packed_goal.shape[1] != 1:
-        raise ValueError("packed_goal must have channel dim = 1")
-    if packed_goal.shape[2:] != packed_obs.shape[2:]:
-        raise ValueError("packed_goal spatial shape mismatch")
+    for name, t in (("packed_obs", packed_obs), ("packed_goal", packed_goal)):
+        if t.dtype is not torch.uint8:
+            raise ValueError(f"{name}: expected uint8 packed frames, got {t.dtype}")
+    # the goal is one frame: [H, W_bytes] with an optional channel and batch of 1
+    goal = packed_goal.reshape(1, 1, *packed_goal.shape[-2:]) if packed_goal.ndim in (2, 3, 4) else None
+    if packed_obs.ndim != 4 or packed_obs.shape[1] != 1:
+        raise ValueError(f"packed_obs: expected [N, 1, H, W_bytes], got {tuple(packed_obs.shape)}")
+    if goal is None or goal.numel() != packed_goal.numel() or goal.shape[2:] != packed_obs.shape[2:]:
+        raise ValueError(
+            f"packed_goal: expected one {tuple(packed_obs.shape[2:])} frame, got {tuple(packed_goal.shape)}"
+        )
+    packed_goal = goal
     o = packed_obs.to(torch.int16)
     g = packed_goal.to(torch.int16)
     d = torch.zeros_like(o)

@@ -1,21 +1,64 @@
-"""Preallocated rollout storage (reference ``src/gbxcule/rl/rollout.py``).
+"""Device storage for one rollout, written in place by the emulator.
 
-Observations live in ``obs_u8[obs_steps, N, stack_k, H, W]``; ``obs_slot(t)``
-is a contiguous view a renderer writes into directly, so a step's pixels are
-never copied.  Same constructor, properties, methods and errors as the
-reference's ``RolloutBuffer``.
+A rollout is a stack of frames plus one row per step of typed columns:
+
+* frames ``[obs_steps, N, stack_k, H, W]`` uint8 (unpacked shades, or packed
+  2-bit bytes with W = 20).  ``obs_slot(t)`` is a contiguous view of one
+  step's frames, so the renderer writes a step's pixels straight into the
+  rollout and nothing is copied;
+* columns ``[steps, N]``: the schema ``COLUMNS`` fixes each column's dtype,
+  and every write is checked against it.
+
+``steps`` counts the rows written so far.  ``obs_steps`` may exceed ``steps``
+so that the frame after the last action (the bootstrap observation) has a
+slot of its own.  The class keeps the name, keyword arguments, attributes and
+methods of the reference's ``RolloutBuffer`` (``src/gbxcule/rl/rollout.py``),
+which the reference's RL engines call.
 """
 
 from __future__ import annotations
 
+from typing import Any
+
 from ..abi import DOWNSAMPLE_H, DOWNSAMPLE_W, DOWNSAMPLE_W_BYTES
 
-# per-step fields: name -> torch dtype attribute
-_FIELDS = (("actions", "int32"), ("rewards", "float32"), ("dones", "bool"),
-           ("values", "float32"), ("logprobs", "float32"))  # fmt: skip
+# per-step columns and their torch dtypes (resolved by name)
+COLUMNS: dict[str, str] = {
+    "actions": "int32",
+    "rewards": "float32",
+    "dones": "bool",
+    "values": "float32",
+    "logprobs": "float32",
+}
+FRAME_FORMATS = ("u8", "packed2")
+
+
+def _positive(**dims: int) -> dict[str, int]:
+    out = {}
+    for name, v in dims.items():
+        if int(v) < 1:
+            raise ValueError(f"{name} has to be at least 1 (got {v})")
+        out[name] = int(v)
+    return out
+
+
+def _frame_shape(obs_format: str, height: int, width: int) -> tuple[int, int]:
+    """(H, W) of one stored frame.  Packed frames hold 4 shades per byte: the
+    unpacked width 80 names the same frame as the packed width 20."""
+    if obs_format not in FRAME_FORMATS:
+        raise ValueError(f"obs_format {obs_format!r} is not one of {FRAME_FORMATS}")
+    h, w = _positive(height=height, width=width).values()
+    if obs_format == "packed2":
+        if w == DOWNSAMPLE_W:
+            w = DOWNSAMPLE_W_BYTES
+        if w != DOWNSAMPLE_W_BYTES:
+            raise ValueError(f"packed2 frames are {DOWNSAMPLE_W_BYTES} bytes wide (got width {width})")
+    return h, w
 
 
 class RolloutBuffer:
+    """Frames and per-step columns of one rollout, preallocated on ``device``."""
+
     def __init__(
         self,
         *,
@@ -30,98 +73,91 @@ class RolloutBuffer:
     ) -> None:
         import torch
 
-        if steps < 1:
-            raise ValueError("steps must be >= 1")
-        if num_envs < 1:
-            raise ValueError("num_envs must be >= 1")
-        if stack_k < 1:
-            raise ValueError("stack_k must be >= 1")
-        if height < 1 or width < 1:
-            raise ValueError("height/width must be >= 1")
-        if obs_format not in ("u8", "packed2"):
-            raise ValueError("obs_format must be 'u8' or 'packed2'")
-        if obs_format == "packed2":
-            width = DOWNSAMPLE_W_BYTES if width == DOWNSAMPLE_W else width
-            if width != DOWNSAMPLE_W_BYTES:
-                raise ValueError("packed2 width must equal DOWNSAMPLE_W_BYTES")
-        self._torch = torch
-        self.steps = int(steps)
-        self.obs_steps = int(steps if obs_steps is None else obs_steps)
+        dims = _positive(steps=steps, num_envs=num_envs, stack_k=stack_k)
+        self.steps, self.num_envs, self.stack_k = dims["steps"], dims["num_envs"], dims["stack_k"]
+        self.obs_steps = self.steps if obs_steps is None else int(obs_steps)
         if self.obs_steps < self.steps:
-            raise ValueError("obs_steps must be >= steps")
-        self.num_envs = int(num_envs)
-        self.stack_k = int(stack_k)
+            raise ValueError(f"obs_steps ({self.obs_steps}) leaves no frame slot for some of the {self.steps} steps")
         self.obs_format = obs_format
-        self.height = int(height)
-        self.width = int(width)
+        self.height, self.width = _frame_shape(obs_format, height, width)
         self.device = torch.device(device)
-        self.obs_u8 = torch.empty(
-            (self.obs_steps, self.num_envs, self.stack_k, self.height, self.width),
-            dtype=torch.uint8,
-            device=self.device,
-        )
-        for name, dt in _FIELDS:
-            setattr(self, name, torch.empty((self.steps, self.num_envs),
-                                            dtype=getattr(torch, dt), device=self.device))  # fmt: skip
-        self._step = 0
+        self._torch = torch
+        self._frame = (self.num_envs, self.stack_k, self.height, self.width)
+        self.obs_u8 = torch.empty((self.obs_steps, *self._frame), dtype=torch.uint8, device=self.device)
+        self._dtypes = {name: getattr(torch, dt) for name, dt in COLUMNS.items()}
+        self._columns = {
+            name: torch.empty((self.steps, self.num_envs), dtype=dt, device=self.device)
+            for name, dt in self._dtypes.items()
+        }
+        self._written = 0
+
+    # columns read as attributes (buffer.actions, buffer.rewards, ...)
+    def __getattr__(self, name: str) -> Any:
+        cols = self.__dict__.get("_columns")
+        if cols is not None and name in cols:
+            return cols[name]
+        raise AttributeError(name)
 
     @property
     def step(self) -> int:
-        return self._step
+        """Rows written since the last ``reset``."""
+        return self._written
 
     @property
     def obs(self):
         return self.obs_u8
 
     def reset(self) -> None:
-        self._step = 0
+        self._written = 0
 
-    def _check_fields(self, values: dict) -> None:
-        torch = self._torch
-        for name, dt in _FIELDS:
-            v = values[name]
-            if v.shape != (self.num_envs,):
-                raise ValueError(f"{name} shape mismatch")
-            if v.dtype is not getattr(torch, dt):
-                raise ValueError(f"{name} must be {dt}")
+    def _check(self, name: str, t, shape: tuple[int, ...], dtype) -> None:
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name}: expected shape {shape}, got {tuple(t.shape)}")
+        if t.dtype is not dtype:
+            raise ValueError(f"{name}: expected dtype {dtype}, got {t.dtype}")
 
-    def add(self, obs_u8, actions, rewards, dones, values, logprobs) -> None:
-        if self._step >= self.steps:
-            raise RuntimeError("rollout buffer is full")
-        if obs_u8.shape != (self.num_envs, self.stack_k, self.height, self.width):
-            raise ValueError("obs_u8 shape mismatch")
-        if obs_u8.dtype is not self._torch.uint8:
-            raise ValueError("obs_u8 must be uint8")
-        fields = dict(actions=actions, rewards=rewards, dones=dones, values=values, logprobs=logprobs)
-        self._check_fields(fields)
-        self.obs_u8[self._step].copy_(obs_u8)
-        for name, v in fields.items():
-            getattr(self, name)[self._step].copy_(v)
-        self._step += 1
+    def _row(self, t: int, values: dict[str, Any]) -> None:
+        """Validate every column first, then write row ``t``."""
+        missing = set(COLUMNS) - set(values)
+        if missing:
+            raise ValueError(f"missing columns {sorted(missing)}")
+        for name, v in values.items():
+            self._check(name, v, (self.num_envs,), self._dtypes[name])
+        for name, v in values.items():
+            self._columns[name][t].copy_(v)
 
     def obs_slot(self, step_idx: int):
-        if step_idx < 0 or step_idx >= self.obs_steps:
-            raise ValueError("step_idx out of range")
+        """Contiguous ``[N, stack_k, H, W]`` view of the frames of step ``step_idx``."""
+        if not 0 <= step_idx < self.obs_steps:
+            raise ValueError(f"step_idx {step_idx} is outside the {self.obs_steps} frame slots")
         return self.obs_u8[step_idx]
 
     def set_step_fields(self, step_idx: int, actions, rewards, dones, values, logprobs) -> None:
-        if step_idx < 0 or step_idx >= self.steps:
-            raise ValueError("step_idx out of range")
-        fields = dict(actions=actions, rewards=rewards, dones=dones, values=values, logprobs=logprobs)
-        self._check_fields(fields)
-        for name, v in fields.items():
-            getattr(self, name)[step_idx].copy_(v)
-        if step_idx == self._step:
-            self._step += 1
+        """Write the columns of step ``step_idx`` (its frame is written in place
+        through ``obs_slot``); writing the next unwritten row advances ``step``."""
+        if not 0 <= step_idx < self.steps:
+            raise ValueError(f"step_idx {step_idx} is outside the {self.steps} rows")
+        self._row(step_idx, dict(actions=actions, rewards=rewards, dones=dones, values=values, logprobs=logprobs))
+        if step_idx == self._written:
+            self._written += 1
 
-    def as_batch(self, *, flatten_obs: bool = True):
-        if self._step != self.steps:
-            raise RuntimeError("rollout buffer is not full")
-        b = self.steps * self.num_envs
-        obs = self.obs_u8[: self.steps]
+    def add(self, obs_u8, actions, rewards, dones, values, logprobs) -> None:
+        """Append one step: copy its frames into the next slot and its columns
+        into the next row."""
+        if self._written == self.steps:
+            raise RuntimeError(f"rollout buffer is full ({self.steps} steps written)")
+        self._check("obs_u8", obs_u8, self._frame, self._torch.uint8)
+        self._row(self._written, dict(actions=actions, rewards=rewards, dones=dones, values=values, logprobs=logprobs))
+        self.obs_u8[self._written].copy_(obs_u8)
+        self._written += 1
+
+    def as_batch(self, *, flatten_obs: bool = True) -> dict[str, Any]:
+        """The full rollout as a batch: steps x envs rows (views, no copies)."""
+        if self._written != self.steps:
+            raise RuntimeError(f"rollout buffer is not full ({self._written} of {self.steps} steps written)")
+        frames = self.obs_u8[: self.steps]
         if flatten_obs:
-            obs = obs.reshape(b, self.stack_k, self.height, self.width)
-        out = {"obs_u8": obs}
-        for name, _ in _FIELDS:
-            out[name] = getattr(self, name).reshape(b)
-        return out
+            frames = frames.reshape(self.steps * self.num_envs, *self._frame[1:])
+        batch = {"obs_u8": frames}
+        batch.update({name: col.reshape(-1) for name, col in self._columns.items()})
+        return batch

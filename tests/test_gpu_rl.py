@@ -6,6 +6,8 @@ and a double-buffer hand-off between an actor and a learner stream."""
 
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 import pytest
 
@@ -158,6 +160,11 @@ def test_render_contract(carts, bootstub):
         b.close()
 
 
+@contextlib.contextmanager
+def _nothing():
+    yield
+
+
 def test_double_buffer_handoff(carts, bootstub):
     """Actor stream renders into buffer i and marks it ready; the learner
     stream waits on that event, consumes it and marks it free."""
@@ -180,17 +187,25 @@ def test_double_buffer_handoff(carts, bootstub):
         torch.cuda.synchronize()
         for it in range(4):
             i = it % 2
+            # iterations 0-1 call the hand-offs one by one, 2-3 as with-blocks
             with torch.cuda.stream(actor):
-                mgr.wait_free(i, actor)
-                for t in range(3):
-                    if t:
-                        b.step_torch(act)
-                    b.render_pixels_snapshot_packed_to_torch(bufs[i].obs_slot(t), 0)
-                mgr.mark_ready(i, actor, policy_version=it)
+                if it < 2:
+                    mgr.wait_free(i, actor)
+                with mgr.filling(i, actor, policy_version=it) if it >= 2 else _nothing():
+                    for t in range(3):
+                        if t:
+                            b.step_torch(act)
+                        b.render_pixels_snapshot_packed_to_torch(bufs[i].obs_slot(t), 0)
+                if it < 2:
+                    mgr.mark_ready(i, actor, policy_version=it)
             with torch.cuda.stream(learner):
-                mgr.wait_ready(i, learner)
-                seen.append(bufs[i].obs.clone())
-                mgr.mark_free(i, learner)
+                if it < 2:
+                    mgr.wait_ready(i, learner)
+                    seen.append(bufs[i].obs.clone())
+                    mgr.mark_free(i, learner)
+                else:
+                    with mgr.reading(i, learner):
+                        seen.append(bufs[i].obs.clone())
         torch.cuda.synchronize()
         assert mgr.policy_version(1) == 3 and mgr.num_buffers == 2
         # consecutive hand-offs continue the same trajectory: the last frame

@@ -58,7 +58,7 @@ def test_set_step_fields_and_batch():
     assert r.as_batch(flatten_obs=False)["obs_u8"].shape == (3, 4, 1, 72, 20)
     bad = _fields(4)
     bad["actions"] = bad["actions"].to(torch.int64)
-    with pytest.raises(ValueError, match="actions must be int32"):
+    with pytest.raises(ValueError, match="actions: expected dtype"):
         r.set_step_fields(0, **bad)
     with pytest.raises(ValueError, match="step_idx"):
         r.set_step_fields(3, **_fields(4))
@@ -76,7 +76,7 @@ def test_add_and_errors():
         _rb().as_batch()
     for kw, msg in ((dict(steps=0), "steps"), (dict(num_envs=0), "num_envs"),
                     (dict(stack_k=0), "stack_k"), (dict(obs_format="rgb"), "obs_format"),
-                    (dict(width=21), "packed2 width"), (dict(obs_steps=2), "obs_steps")):  # fmt: skip
+                    (dict(width=21), "packed2 frames"), (dict(obs_steps=2), "obs_steps")):  # fmt: skip
         with pytest.raises(ValueError, match=msg):
             _rb(**kw)
 
