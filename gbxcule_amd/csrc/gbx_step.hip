@@ -156,7 +156,10 @@ struct Lane {
   int rtc_sub;
   uint32_t rtc_halt, rtc_dirty;
   uint32_t map_changed;  // set when a write remaps the fetch windows
-  int budget;            // cycles a fast-path step may take (event_budget)
+  // Cycles a step may take on the fast path (event_budget).  Every event the
+  // fast path must not pass sets it to 0: writes with side effects, MBC and
+  // RTC writes, traps; the slow path recomputes it.
+  int budget;
   // frame loop
   int frames_done, release;
   int32_t action;
@@ -535,6 +538,7 @@ struct Lane {
     }
     refresh_cart();
     map_changed = 1;
+    budget = 0;
   }
   __device__ void write_special(uint32_t x, uint32_t v) {
     if (x < 0x8000u) {
@@ -544,6 +548,7 @@ struct Lane {
       if (rtc_field >= 0) {
         CS(CS_RTC_SECONDS + rtc_field) = (int)v;
         rtc_dirty = 1;
+        budget = 0;
         if (rtc_field == 4) rtc_halt = (v & 0x40u) ? 1u : 0u;
         return;
       }
@@ -567,13 +572,21 @@ struct Lane {
     if (!write_is_special(x) & (x != 0xFF00u)) M(x) = v;
     else write_special(x, v);
   }
-  // The instruction's bus writes, in order (n = 0, 1 or 2).  When none is
-  // special both are plain stores without a branch; a lane with one write
+  // Addresses a write reaches as a plain byte store without side effects:
+  // video RAM, work RAM, high RAM (FF80-FFFE), and FF00, whose store is the
+  // joypad value for the written select bits.  Everything else (ROM/MBC
+  // registers, cartridge RAM, echo RAM, OAM, IO registers, IE) goes through
+  // write8.  x is a 16-bit address.
+  __device__ static bool plain_store(uint32_t x) {
+    return (((0x3300u >> (x >> 12)) & 1u) != 0u) | (x - 0xFF80u < 0x7Fu) | (x == 0xFF00u);
+  }
+  // The instruction's bus writes, in order (n = 0, 1 or 2).  When both are
+  // plain stores they are stored without a branch; a lane with one write
   // stores its first byte twice.
   __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1) {
-    const uint32_t x0 = fold(a0), x1 = fold(a1);
+    const uint32_t x0 = a0 & 0xFFFFu, x1 = a1 & 0xFFFFu;
     const bool two = n >= 2u;
-    if (__builtin_expect(write_is_special(x0) | (two & write_is_special(x1)), 0)) {
+    if (__builtin_expect((!plain_store(x0)) | (two & !plain_store(x1)), 0)) {
       write8(a0, v0);
       if (two) write8(a1, v1);
     } else {
@@ -624,31 +637,79 @@ struct Lane {
     return stat_bits(mode_now(sc), ly == lyc_pp ? 1u : 0u);
   }
   // Line change(s) after scan reached 456; s0 = scanline cycle before the step.
+  // The reference applies each change in turn (cpu_step_builder.py:1436-
+  // 1480).  A run of m >= 2 changes, the batched steps of a halted CPU, an LY
+  // poll or a block copy, is applied in closed form (ppu_lines_run) unless
+  // this is env 0, whose scanline latches record every line.
   __device__ void ppu_lines(uint32_t s0) {
     uint32_t prev = stat_prev_at(s0);
-    const uint32_t lc = lcdc;
-    uint32_t total = scan;
-    while (total >= (uint32_t)kCyclesPerLine) {
-      total -= kCyclesPerLine;
-      const uint32_t pl = ly;
-      wl += (uint32_t)((pl < (uint32_t)kScreenH) & ((lc & 0x20u) != 0u) & (pl >= wy));
-      uint32_t nl = ly + 1u;
-      if (nl >= (uint32_t)kLinesPerFrame) nl %= (uint32_t)kLinesPerFrame;
-      ly = nl;
-      wl = ly == 0u ? 0u : wl;
-      lym = ly;
-      // ppu_update_stat_irq with mode 0 or 1: bit0 mode 0, bit1 mode 1, bit3 LY == LYC
-      const uint32_t vb = ly >= (uint32_t)kScreenH ? 1u : 0u;
-      const uint32_t cur = (1u << vb) | ((ly == lyc ? 1u : 0u) << 3);
-      const uint32_t en = (stat_full >> 3) & 0xFu;  // bit0 mode0, 1 mode1, 2 mode2, 3 lyc
-      ifr |= (uint32_t)((en & cur & ~(prev & 0xFu)) != 0u) << 1;
-      prev = cur;
-      ifr |= (uint32_t)((pl == 143u) & (ly == 144u));
-      if ((e == 0u) & (ly < (uint32_t)kScreenH)) latch_env0();
+    const uint32_t m = scan / (uint32_t)kCyclesPerLine;
+    {
+      const uint32_t lc = lcdc;
+      uint32_t total = scan;
+      while (total >= (uint32_t)kCyclesPerLine) {
+        total -= kCyclesPerLine;
+        const uint32_t pl = ly;
+        wl += (uint32_t)((pl < (uint32_t)kScreenH) & ((lc & 0x20u) != 0u) & (pl >= wy));
+        uint32_t nl = ly + 1u;
+        if (nl >= (uint32_t)kLinesPerFrame) nl %= (uint32_t)kLinesPerFrame;
+        ly = nl;
+        wl = ly == 0u ? 0u : wl;
+        lym = ly;
+        // ppu_update_stat_irq with mode 0 or 1: bit0 mode 0, bit1 mode 1, bit3 LY == LYC
+        const uint32_t vb = ly >= (uint32_t)kScreenH ? 1u : 0u;
+        const uint32_t cur = (1u << vb) | ((ly == lyc ? 1u : 0u) << 3);
+        const uint32_t en = (stat_full >> 3) & 0xFu;  // bit0 mode0, 1 mode1, 2 mode2, 3 lyc
+        ifr |= (uint32_t)((en & cur & ~(prev & 0xFu)) != 0u) << 1;
+        prev = cur;
+        ifr |= (uint32_t)((pl == 143u) & (ly == 144u));
+        if ((e == 0u) & (ly < (uint32_t)kScreenH)) latch_env0();
+      }
+      scan = total;
     }
-    scan = total;
     M(0xFF44) = lym;
     M(0xFF0F) = ifr;
+  }
+  // m line changes (2 <= m <= 154) from line ly < 154, with LCDC, STAT, LYC
+  // and WY fixed over the run.  Change j enters line l_j = (ly + j) % 154
+  // having left l_{j-1}; line t is entered at change j_t = (t - ly - 1) % 154
+  // + 1, once, so it is entered in the run iff j_t <= m.  Then:
+  //  * the window line counter counts the lines left below 144 and at or
+  //    past WY (LCDC bit 5), restarting at 0 when line 0 is entered;
+  //  * VBlank is requested iff line 144 is entered (always from line 143);
+  //  * a STAT request is raised iff the first change shows an enabled bit
+  //    that prev (the bits before the run) lacks, or a later change enters
+  //    line 144 (mode-1 source: the line before is below 144), line 0
+  //    (mode-0 source: the line before is 153) or line LYC (LYC source:
+  //    neighbouring lines differ).  The mode-2 bit is never current at a
+  //    change.
+  __device__ void ppu_lines_run(uint32_t m, uint32_t prev) {
+    const uint32_t nl = (uint32_t)kLinesPerFrame;
+    auto entered_at = [&](uint32_t t) {  // j_t for t < 154
+      const uint32_t x = t + (nl - 1u) - ly;  // 0 .. 306
+      return (x >= nl ? x - nl : x) + 1u;
+    };
+    const uint32_t en = (stat_full >> 3) & 0xFu;
+    const uint32_t l1 = ly + 1u == nl ? 0u : ly + 1u;
+    const uint32_t cur1 = (1u << (l1 >= (uint32_t)kScreenH ? 1u : 0u)) | ((l1 == lyc ? 1u : 0u) << 3);
+    const uint32_t j144 = entered_at(144u), j0 = entered_at(0u);
+    const uint32_t jl = lyc < nl ? entered_at(lyc) : 0xFFFFu;
+    const bool stat = ((en & cur1 & ~(prev & 0xFu)) != 0u) | (((en & 2u) != 0u) & (j144 >= 2u) & (j144 <= m)) |
+                      (((en & 1u) != 0u) & (j0 >= 2u) & (j0 <= m)) |
+                      (((en & 8u) != 0u) & (jl >= 2u) & (jl <= m));
+    ifr |= ((uint32_t)stat << 1) | (uint32_t)(j144 <= m);
+    uint32_t lf = ly + m;  // <= 307
+    lf = lf >= nl ? lf - nl : lf;
+    const bool wrapped = j0 <= m;
+    // lines in [a, b) below 144 and at or past WY, with the window on
+    auto counted = [&](uint32_t a, uint32_t b) {
+      const int hi = min((int)b, kScreenH), lo = max((int)a, (int)wy);
+      return (lcdc & 0x20u) && hi > lo ? (uint32_t)(hi - lo) : 0u;
+    };
+    wl = wrapped ? counted(0u, lf) : wl + counted(ly, lf);
+    ly = lf;
+    lym = lf;
+    scan -= m * (uint32_t)kCyclesPerLine;
   }
   // One PPU step of `cycles` (cycles > 0).
   __device__ uint32_t ppu_advance(int cycles) {
@@ -802,9 +863,12 @@ struct Lane {
     int b = kCyclesPerFrame - cframe;
     const uint32_t te = tmask - (div & 0xFFFFu & tmask);
     b = te < (uint32_t)b ? (int)te + 1 : b;
-    if (lcdc & 0x80u) b = min(b, kCyclesPerLine - (int)scan);
-    else if ((scan | ly | wl | lym) != 0u) b = 0;
-    return b;
+    b = (lcdc & 0x80u) ? min(b, kCyclesPerLine - (int)scan) : ((scan | ly | wl | lym) != 0u ? 0 : b);
+    if ((mbc == MBC_MBC3) & (rtc_halt == 0u))  // the next RTC second
+      b = ((rtc_dirty != 0u) | (rtc_sub < 0)) ? 0 : min(b, kRtcCyclesPerSecond - rtc_sub);
+    // a pending TIMA reload, EI delay, interrupt request or bank remap takes
+    // the full sequence every step until it is dealt with
+    return (pend | ime_delay | (ie & ifr & 0x1Fu) | map_changed) != 0u ? 0 : b;
   }
   // Cycles a halted CPU advances in one loop iteration: the reference steps
   // 4 cycles at a time and wakes on IE & IF; nothing it can observe changes
@@ -828,6 +892,15 @@ struct Lane {
   __device__ uint32_t rec_index(uint32_t p) const {
     return ((boot_en != 0u) & (p < 0x100u)) ? rom_len + p
                                    : (p < 0x4000u ? rom_lo : rom_hi) + (p & 0x3FFFu);
+  }
+  // rec_ok and rec_index in one: the record index for p, or 0 when no record
+  // serves it (ok false).  Written as selects so that the per-instruction
+  // path has no branch for it.
+  __device__ uint32_t next_rec(uint32_t p, bool& ok) const {
+    const bool bw = (boot_en != 0u) & (p < 0x100u);
+    const uint32_t win = sel(p < 0x4000u, rom_lo, rom_hi) + (p & 0x3FFFu);
+    ok = (bw & (p < 0xFEu)) | (!bw & (p < 0x8000u) & ((p & 0x3FFFu) <= 0x3FFDu));
+    return sel(ok, sel(bw, rom_len + p, win), 0u);
   }
   // Fetch + decode through the bus (code in RAM, window edges, open bus).
   __device__ Rec fetch_slow() const {
@@ -1034,6 +1107,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
           trap_pc = (int)pc;
           trap_op = (int)op;
           trap_kind = 1;
+          L.budget = 0;
         }
         if (!dbg && (o.misc & 16u) && (rec.w[15] & kCopyLoop)) {
           // LD A,(HL+) of a block-copy loop just ran: advance k whole passes
@@ -1075,8 +1149,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       }
       L.pc = npc;
       // fetch the next record while the writes, timer and PPU run
-      rv = L.rec_ok(npc);
-      load_rec(rv ? L.rec_index(npc) : 0u);
+      load_rec(L.next_rec(npc, rv));
       }
     } else {
       cycles = L.halt_cycles(cframe);
@@ -1105,21 +1178,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     // Fast path: when no timer edge or reload, no scanline wrap, no LCD
     // switch, no pending interrupt, no remap, no RTC second and no frame end
     // fall inside this step, the sequence below reduces to DIV, the scanline
-    // position and the cycle counters advancing; one test covers all of it.
+    // position and the cycle counters advancing.  The budget is the distance
+    // to the nearest of those events, and 0 while any of them is pending or
+    // once this step made one (an IO, MBC or RTC write, a trap).
     const uint32_t lc_now = L.lcdc;
     const uint32_t ucyc = (uint32_t)cycles;
     const bool lcd_on = (lc_now & 0x80u) != 0u;
-    bool fast = (trap == 0) & (L.pend == 0u) & (cycles < L.budget) & (L.ime_delay == 0u) &
-                ((L.ie & L.ifr & 0x1Fu) == 0u) & (L.map_changed == 0u) & (((lcdc_prev ^ lc_now) & 0x80u) == 0u);
-    if (kMbc == MBC_MBC3)
-      fast = fast & ((L.rtc_halt != 0u) | ((L.rtc_sub >= 0) & (L.rtc_sub + cycles < kRtcCyclesPerSecond) &
-                                           (L.rtc_dirty == 0u)));
+    const bool fast = (trap == 0) & (cycles < L.budget);
     if (__builtin_expect(fast, 1)) {
+      // stat_fresh, lyc_pp and lcd_pp already hold what a PPU step would set:
+      // STAT, LYC and LCDC writes go through io_write, which zeroes the
+      // budget, and a launch starts with the budget at 0
       L.div = (L.div + ucyc) & 0xFFFFu;
       L.scan = lcd_on ? L.scan + ucyc : 0u;
-      L.stat_fresh = 0;
-      L.lyc_pp = L.lyc;
-      L.lcd_pp = lc_now & 0x80u;
       if (kMbc == MBC_MBC3) L.rtc_sub += L.rtc_halt ? 0 : cycles;
       ncyc += ucyc;
       cframe += cycles;
