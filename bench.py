@@ -51,6 +51,17 @@ TARGETS = {  # env-steps/s the C4 131K target names, per frameskip
 }
 
 
+
+def wl_label(wl, default) -> str:
+    """The registry name of a workload, with the env count and frameskip it
+    ran at when they differ from the registry's."""
+    name = wl.name
+    if wl.num_envs != default.num_envs:
+        name = name.rsplit("_", 1)[0] + f"_{wl.num_envs}envs"
+    if wl.frames_per_step != default.frames_per_step:
+        name += f"_fs{wl.frames_per_step}"
+    return name
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -286,10 +297,12 @@ def main() -> int:
         for key, wname, en, efs, esteps in EXTRA:
             ewl = replace(WORKLOADS[wname], num_envs=en, frames_per_step=efs)
             r = time_workload(ewl, esteps, args.warmup)
-            _, _, db, ib = oracle_sample(ewl, ewl.rom(), boot, 64, 0.0, cpu_threads()[0], max_steps=1)
+            # the same 24 emulated frames as one frameskip-24 step
+            _, _, db, ib = oracle_sample(ewl, ewl.rom(), boot, 64, 0.0, cpu_threads()[0],
+                                         max_steps=max(1, 24 // efs))
             r["roofline"] = roofline(wname, r, db, ib)
             r["valu"] = valu_object(wname, r)
-            r["workload"] = ewl.name
+            r["workload"] = key
             tgt = TARGETS.get((wname, en, efs))
             if tgt:
                 r["target"] = tgt
@@ -300,7 +313,7 @@ def main() -> int:
     threads, avail = cpu_threads()
     cpu = None
     if args.no_cpu_baseline:
-        _, _, data_b, instr_b = oracle_sample(wl, rom, boot, 64, 0.0, threads, max_steps=1)
+        _, _, data_b, instr_b = oracle_sample(wl, rom, boot, 64, 0.0, threads, max_steps=max(1, 24 // fs))
     else:
         n_cpu = min(n, 64 * threads)
         c_steps, c_dt, data_b, instr_b = oracle_sample(wl, rom, boot, n_cpu, args.cpu_seconds, threads)
@@ -332,7 +345,7 @@ def main() -> int:
         "dtype": "u8",
         "data": "synthetic",
         "config": {
-            "workload": wl.name,
+            "workload": wl_label(wl, WORKLOADS[args.workload]),
             "num_envs": n,
             "frameskip": fs,
             "release_after_frames": wl.release_after_frames,
