@@ -18,6 +18,21 @@ LIB_DIR = PKG / "lib"
 LIB_PATH = LIB_DIR / "libgbx_hip.so"
 SOURCES = ("gbx_step.hip", "gbx_aux.hip", "gbx_api.hip")
 ARCH = os.environ.get("GBX_OFFLOAD_ARCH", "gfx950")
+# -O2 with the iterative ILP machine scheduler: on the step kernel's hot
+# loop this schedules the dependent loads earlier than -O3 with the default
+# occupancy-first scheduler (same-box A/B: 16K-env CPU-step workload +2.4%,
+# 131K-env banked cart +2.5%, RL rollout shape unchanged).
+DEVICE_FLAGS = (
+    "-O2",
+    f"--offload-arch={ARCH}",
+    "-std=c++17",
+    "-mllvm",
+    "-amdgpu-sched-strategy=iterative-ilp",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+)
 
 
 def hipcc() -> str:
@@ -33,15 +48,9 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB_DIR / "libgbx_hip.so.tmp"
     cmd = [
         hipcc(),
-        "-O3",
-        f"--offload-arch={ARCH}",
-        "-std=c++17",
+        *DEVICE_FLAGS,
         "-fPIC",
         "-shared",
-        "-Xclang",
-        "-target-feature",
-        "-Xclang",
-        "-packed-fp32-ops",
         "-I",
         str(PKG.parent / "include"),
         "-o",

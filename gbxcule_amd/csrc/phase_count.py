@@ -25,6 +25,8 @@ from pathlib import Path
 
 CSRC = Path(__file__).resolve().parent
 INCLUDE = CSRC.parent.parent / "include"
+sys.path.insert(0, str(CSRC.parent))
+from build import DEVICE_FLAGS  # noqa: E402  (the flags the library is built with)
 KERNEL = "_ZN3gbx12_GLOBAL__N_111step_kernelILi0ELb0E"  # step_kernel<MBC_ROM_ONLY, false>
 PHASES = ("fetch", "bus", "exec", "nextrec", "write", "tail", "loop")
 LABELS = {
@@ -85,8 +87,8 @@ def marked_sources(dst: Path) -> None:
 
 def assemble(src: Path, out: Path) -> list[str]:
     subprocess.run(
-        ["/opt/rocm/bin/hipcc", "-O3", "--offload-arch=gfx950", "-std=c++17", "--cuda-device-only", "-S",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", str(INCLUDE), "-o", str(out), str(src)],
+        ["/opt/rocm/bin/hipcc", *DEVICE_FLAGS, "--cuda-device-only", "-S", "-I", str(INCLUDE), "-o", str(out),
+         str(src)],
         check=True, stderr=subprocess.DEVNULL)
     lines = out.read_text().split("\n")
     st = next(i for i, x in enumerate(lines) if x.startswith(KERNEL))
