@@ -92,7 +92,8 @@ def cpu_threads() -> tuple[int, int]:
 
 
 def oracle_sample(wl, rom, boot, n_env, seconds, threads, max_steps=200):
-    """Time the oracle on envs [0, n_env) of the workload's own trace."""
+    """Time the oracle on envs [0, n_env) of the workload's own trace: up to
+    ``max_steps`` steps, stopping early once ``seconds`` (if > 0) have passed."""
     from gbxcule_amd.carts.synth import seeded_actions
     from oracle.ref import RefMachine
 
@@ -106,7 +107,7 @@ def oracle_sample(wl, rom, boot, n_env, seconds, threads, max_steps=200):
         if wl.render:
             ref.render(packed=wl.render == "packed", threads=threads)
         steps += 1
-        if time.perf_counter() - t0 >= seconds:
+        if seconds > 0 and time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
     data_per_env_step = float(ref.data_bytes.sum()) / (n_env * steps)
@@ -181,6 +182,7 @@ def time_workload(wl, steps: int, warmup: int) -> dict:
         for k in range(warmup):
             one_step(k)
         torch.cuda.synchronize()
+        instr0 = int(be.export_field("instr_count").sum())
         # the kernel runs on torch's current stream, where these events record
         events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                   for _ in range(steps)]
@@ -191,6 +193,8 @@ def time_workload(wl, steps: int, warmup: int) -> dict:
         elapsed = time.perf_counter() - t0
         kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in events]))
         value = n * steps / elapsed
+        # emulated instructions retired by the timed steps (device counters)
+        instr_timed = int(be.export_field("instr_count").sum()) - instr0
         return {
             "value": value,
             "unit": "env-steps/s",
@@ -201,7 +205,8 @@ def time_workload(wl, steps: int, warmup: int) -> dict:
             "ms_per_step": elapsed / steps * 1e3,
             "step_kernel_ms": kernel_ms,
             "frames_per_sec": value * fs,
-            "emulated_instr_per_sec": float(be.export_field("instr_count").sum()) / total / (elapsed / steps),
+            "emulated_instr_per_sec": instr_timed / elapsed,
+            "emulated_instr_per_env_step": instr_timed / (n * steps),
             "traps": int(be.export_field("trap_flag").sum()),
             "step_lanes": be.step_lanes,
         }
@@ -360,6 +365,7 @@ def main() -> int:
         },
         "frames_per_sec": res["frames_per_sec"],
         "emulated_instr_per_sec": res["emulated_instr_per_sec"],
+        "emulated_instr_per_env_step": res["emulated_instr_per_env_step"],
         "step_kernel_ms": res["step_kernel_ms"],
         "traps": res["traps"],
         "roofline": roofline(args.workload, res, data_b, instr_b),
