@@ -379,47 +379,69 @@ __global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int wi
   if (i < 2u) snap.cnt[i] = s.cnt[cnt_index(env, (int)i)];
 }
 
-// Masked restore of the interleaved images (mem + cart RAM).  One wavefront
-// per (64-env block, chunk of address rows): the lanes run over the chunk's
-// rows.  A masked env's byte shares its 64-byte row with the other 63 envs
-// of the block, so restoring it costs a read and a write-back of the row;
-// each lane therefore reads the env's current bytes first (8 rows at a time,
-// loads ahead of any store) and stores only the bytes that differ from the
-// snapshot, so rows that already hold the snapshot byte are never written.
-// Rows below first_row are not restored (the caller knows they already
-// match).  Blocks without a masked env leave at once.
-constexpr uint32_t kResetRows = 4096;
-constexpr int kResetBatch = 8;
-__global__ __launch_bounds__(kEnvBlock) void masked_mem_kernel(DevState s, const uint8_t* snap_mem,
-                                                               const uint8_t* snap_cram,
-                                                               const uint8_t* mask, uint32_t first_row) {
-  const uint32_t b = blockIdx.x, l = threadIdx.x;
-  const uint32_t e = (b << kEnvBlockShift) | l;
+// Masked restore of the interleaved images (mem + cart RAM).  An address
+// row holds one byte of each of the block's 64 envs, so the restore works
+// on whole rows: four lanes (a quad) take one 64-byte row, 16 envs each,
+// load it with one 16-byte load per lane, put the snapshot byte into the
+// positions of the masked envs (a byte mask built once from the block's
+// mask bits) and store the row back, as four 16-byte stores covering all 64
+// bytes, only when one of its bytes changed.  Every masked env of the block
+// is restored in the same pass, each row is read once, and no row is written
+// partially.  A workgroup of 256 threads covers kResetRows rows of one block,
+// four rows per thread in flight.  Rows below first_row are not restored
+// (the caller knows they already match).  Blocks without a masked env leave
+// at once.
+constexpr uint32_t kResetRows = 1024;
+constexpr int kResetBatch = 4;
+__global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8_t* snap_mem,
+                                                         const uint8_t* snap_cram, const uint8_t* mask,
+                                                         uint32_t first_row) {
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  const uint32_t e = (b << kEnvBlockShift) | (t & (kEnvBlock - 1));
   const uint64_t bits = __ballot(e < (uint32_t)s.n && mask[e] != 0);
   if (bits == 0) return;
+  // this lane's 16 envs (16k .. 16k + 15 of the block) as a byte mask
+  const uint32_t k = t & 3u;
+  const uint32_t m16 = (uint32_t)(bits >> (16u * k)) & 0xFFFFu;
+  uint32_t mw[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t n4 = (m16 >> (4 * j)) & 0xFu;
+    mw[j] = ((n4 & 1u) ? 0xFFu : 0u) | ((n4 & 2u) ? 0xFF00u : 0u) | ((n4 & 4u) ? 0xFF0000u : 0u) |
+            ((n4 & 8u) ? 0xFF000000u : 0u);
+  }
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t a0 = first_row + blockIdx.y * kResetRows + l;
-  const uint32_t a1 = min(per_env, first_row + (blockIdx.y + 1u) * kResetRows);
-  for (uint64_t qb = bits; qb; qb &= qb - 1) {
-    const uint32_t q = (uint32_t)__builtin_ctzll(qb);
-    for (uint32_t a = a0; a < a1; a += kEnvBlock * kResetBatch) {
-      uint8_t* p[kResetBatch];
-      uint32_t want[kResetBatch], cur[kResetBatch];
+  const uint32_t r0 = first_row + blockIdx.y * kResetRows + (t >> 2);
+  const uint32_t r1 = min(per_env, first_row + (blockIdx.y + 1u) * kResetRows);
+  const size_t cram_base = (size_t)b * (size_t)s.cram_stride;
+  for (uint32_t r = r0; r < r1; r += 64u * kResetBatch) {
+    uint4* p[kResetBatch];
+    uint4 cur[kResetBatch];
+    uint32_t w[kResetBatch];
 #pragma unroll
-      for (int i = 0; i < kResetBatch; ++i) {
-        const uint32_t ai = a + (uint32_t)i * kEnvBlock;
-        const bool ok = ai < a1;
-        const bool in_mem = ai < (uint32_t)kMemSize;
-        const uint32_t off = ai - (uint32_t)kMemSize;
-        p[i] = !ok ? nullptr
-                   : in_mem ? s.mem + mem_index((b << kEnvBlockShift) | q, ai)
-                            : s.cram + cram_index((b << kEnvBlockShift) | q, off, (uint32_t)s.cram_stride);
-        want[i] = !ok ? 0u : in_mem ? snap_mem[ai] : snap_cram[off];
-        cur[i] = ok ? *p[i] : 0u;
-      }
+    for (int i = 0; i < kResetBatch; ++i) {
+      const uint32_t ri = r + 64u * (uint32_t)i;
+      const bool ok = ri < r1;
+      const bool in_mem = ri < (uint32_t)kMemSize;
+      const uint32_t off = ri - (uint32_t)kMemSize;
+      uint8_t* row = in_mem ? s.mem + ((size_t)b << 22) + ((size_t)ri << kEnvBlockShift)
+                            : s.cram + ((cram_base + off) << kEnvBlockShift);
+      p[i] = ok ? reinterpret_cast<uint4*>(row) + k : nullptr;
+      w[i] = (ok ? (uint32_t)(in_mem ? snap_mem[ri] : snap_cram[off]) : 0u) * 0x01010101u;
+      cur[i] = ok ? *p[i] : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-      for (int i = 0; i < kResetBatch; ++i)
-        if (p[i] != nullptr && cur[i] != want[i]) *p[i] = (uint8_t)want[i];
+    for (int i = 0; i < kResetBatch; ++i) {
+      uint4 nv;
+      nv.x = (cur[i].x & ~mw[0]) | (w[i] & mw[0]);
+      nv.y = (cur[i].y & ~mw[1]) | (w[i] & mw[1]);
+      nv.z = (cur[i].z & ~mw[2]) | (w[i] & mw[2]);
+      nv.w = (cur[i].w & ~mw[3]) | (w[i] & mw[3]);
+      uint32_t d = (nv.x ^ cur[i].x) | (nv.y ^ cur[i].y) | (nv.z ^ cur[i].z) | (nv.w ^ cur[i].w);
+      // the row changed if any of its quad's lanes changed (quad_perm OR)
+      d |= (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0xB1, 0xF, 0xF, true);
+      d |= (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0x4E, 0xF, 0xF, true);
+      if (p[i] != nullptr && d != 0u) *p[i] = nv;
     }
   }
 }
@@ -606,7 +628,7 @@ hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const u
   const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
   const uint32_t chunks = (per_env - (uint32_t)first_row + kResetRows - 1) / kResetRows;
   hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + kEnvBlock - 1) / kEnvBlock), chunks),
-                     dim3(kEnvBlock), 0, st, s, snap.mem, snap.cram, mask, (uint32_t)first_row);
+                     dim3(256), 0, st, s, snap.mem, snap.cram, mask, (uint32_t)first_row);
   hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)s.n), dim3(256), 0, st, s, snap, mask,
                      snap.has_pix);
   return hipGetLastError();
