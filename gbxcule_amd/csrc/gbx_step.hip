@@ -643,8 +643,10 @@ struct Lane {
   // this is env 0, whose scanline latches record every line.
   __device__ void ppu_lines(uint32_t s0) {
     uint32_t prev = stat_prev_at(s0);
-    const uint32_t m = scan / (uint32_t)kCyclesPerLine;
-    {
+    // (the run test is one compare; C2-like code never takes it)
+    if (__builtin_expect((scan >= 2u * (uint32_t)kCyclesPerLine) & (e != 0u), 0)) {
+      ppu_lines_run(scan / (uint32_t)kCyclesPerLine, prev);
+    } else {
       const uint32_t lc = lcdc;
       uint32_t total = scan;
       while (total >= (uint32_t)kCyclesPerLine) {
