@@ -601,18 +601,44 @@ struct Lane {
   }
 
   // -- PPU line bookkeeping (cpu_step_builder.py:421-524, 1406-1500) -----------
+  // The registers env 0 latches for line l: LCDC, SCX, SCY, BGP, WX, WY,
+  // the window line w, OBP0, OBP1.  `io` holds SCX | SCY << 8 | BGP << 16 |
+  // WX << 24 and `obp` OBP0 | OBP1 << 8, as read from memory.
+  __device__ void store_latches(uint32_t l, uint32_t w, uint32_t io, uint32_t obp) const {
+    uint8_t* Lt = s.latches;
+    Lt[0 * kScreenH + l] = (uint8_t)lcdc;
+    Lt[1 * kScreenH + l] = (uint8_t)io;
+    Lt[2 * kScreenH + l] = (uint8_t)(io >> 8);
+    Lt[3 * kScreenH + l] = (uint8_t)(io >> 16);
+    Lt[4 * kScreenH + l] = (uint8_t)(io >> 24);
+    Lt[5 * kScreenH + l] = (uint8_t)wy;
+    Lt[6 * kScreenH + l] = (uint8_t)(w & 0xFFu);
+    Lt[7 * kScreenH + l] = (uint8_t)obp;
+    Lt[8 * kScreenH + l] = (uint8_t)(obp >> 8);
+  }
+  __device__ uint32_t latch_io() const {
+    return (uint32_t)M(0xFF43) | ((uint32_t)M(0xFF42) << 8) | ((uint32_t)M(0xFF47) << 16) |
+           ((uint32_t)M(0xFF4B) << 24);
+  }
+  __device__ uint32_t latch_obp() const { return (uint32_t)M(0xFF48) | ((uint32_t)M(0xFF49) << 8); }
   __device__ void latch_env0() {
     if (e != 0 || ly >= (uint32_t)kScreenH) return;
-    uint8_t* Lt = s.latches;
-    Lt[0 * kScreenH + ly] = (uint8_t)lcdc;
-    Lt[1 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF43);
-    Lt[2 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF42);
-    Lt[3 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF47);
-    Lt[4 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF4B);
-    Lt[5 * kScreenH + ly] = (uint8_t)wy;
-    Lt[6 * kScreenH + ly] = (uint8_t)(wl & 0xFFu);
-    Lt[7 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF48);
-    Lt[8 * kScreenH + ly] = (uint8_t)(uint32_t)M(0xFF49);
+    store_latches(ly, wl, latch_io(), latch_obp());
+  }
+  // Env 0's latches for the visible lines entered by a run of m line
+  // changes from line ly (the run's registers are fixed: no IO write falls
+  // between the lines of one step, so they are read once), with the window
+  // line counter as each change leaves it.
+  __device__ void latch_run(uint32_t m) const {
+    const uint32_t io = latch_io(), obp = latch_obp();
+    const bool win = (lcdc & 0x20u) != 0u;
+    uint32_t l = ly, w = wl;
+    for (uint32_t j = 0; j < m; ++j) {
+      w += (uint32_t)((l < (uint32_t)kScreenH) & win & (l >= wy));
+      l = l + 1u == (uint32_t)kLinesPerFrame ? 0u : l + 1u;
+      w = l == 0u ? 0u : w;
+      if (l < (uint32_t)kScreenH) store_latches(l, w, io, obp);
+    }
   }
   // STAT mode of the current position (LCD on)
   __device__ uint32_t mode_now(uint32_t sc) const {
@@ -639,13 +665,15 @@ struct Lane {
   // Line change(s) after scan reached 456; s0 = scanline cycle before the step.
   // The reference applies each change in turn (cpu_step_builder.py:1436-
   // 1480).  A run of m >= 2 changes, the batched steps of a halted CPU, an LY
-  // poll or a block copy, is applied in closed form (ppu_lines_run) unless
-  // this is env 0, whose scanline latches record every line.
+  // poll or a block copy, is applied in closed form (ppu_lines_run), after
+  // env 0 has recorded the run's scanline latches (latch_run).
   __device__ void ppu_lines(uint32_t s0) {
     uint32_t prev = stat_prev_at(s0);
     // (the run test is one compare; C2-like code never takes it)
-    if (__builtin_expect((scan >= 2u * (uint32_t)kCyclesPerLine) & (e != 0u), 0)) {
-      ppu_lines_run(scan / (uint32_t)kCyclesPerLine, prev);
+    if (__builtin_expect(scan >= 2u * (uint32_t)kCyclesPerLine, 0)) {
+      const uint32_t m = scan / (uint32_t)kCyclesPerLine;
+      if (e == 0u) latch_run(m);
+      ppu_lines_run(m, prev);
     } else {
       const uint32_t lc = lcdc;
       uint32_t total = scan;
