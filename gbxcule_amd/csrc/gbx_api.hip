@@ -251,7 +251,7 @@ int gbx_create(int32_t num_envs, const uint8_t* rom, int64_t rom_len, const uint
   A(dalloc(&s.reward, (size_t)num_envs));
   A(dalloc(&s.pix, (size_t)num_envs * kDsW * kDsH));
   A(dalloc(&s.pix_packed, (size_t)num_envs * kDsWB * kDsH));
-  A(dalloc(&s.latches, (size_t)9 * kScreenH));
+  A(dalloc(&s.latches, (size_t)kScreenH * kLatchStride));
   A(dalloc(&s.frame_bg, (size_t)kScreenW * kScreenH));
   uint8_t *drom = nullptr, *dboot = nullptr;
   Rec* drecs = nullptr;
@@ -319,7 +319,7 @@ int gbx_reset(gbx_ctx* ctx, void* stream) {
   HIP_TRY(hipMemsetAsync(s.reward, 0, (size_t)s.n * sizeof(float), st));
   HIP_TRY(hipMemsetAsync(s.pix, 0, (size_t)s.n * kDsW * kDsH, st));
   HIP_TRY(hipMemsetAsync(s.pix_packed, 0, (size_t)s.n * kDsWB * kDsH, st));
-  HIP_TRY(hipMemsetAsync(s.latches, 0, 9 * kScreenH, st));
+  HIP_TRY(hipMemsetAsync(s.latches, 0, (size_t)kScreenH * kLatchStride, st));
   HIP_TRY(hipMemsetAsync(s.frame_bg, 0, (size_t)kScreenW * kScreenH, st));
   HIP_TRY(launch_reset(s, st));
   return GBX_OK;
@@ -571,7 +571,10 @@ int gbx_export_latches(gbx_ctx* ctx, uint8_t* host_out) {
   CHECK_CTX(ctx);
   if (!host_out) return fail(GBX_E_INVALID, "out is NULL");
   HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemcpy(host_out, ctx->s.latches, 9 * kScreenH, hipMemcpyDeviceToHost));
+  uint8_t lines[kScreenH * kLatchStride];
+  HIP_TRY(hipMemcpy(lines, ctx->s.latches, sizeof(lines), hipMemcpyDeviceToHost));
+  for (int k = 0; k < 9; ++k)
+    for (int y = 0; y < kScreenH; ++y) host_out[k * kScreenH + y] = lines[y * kLatchStride + k];
   return GBX_OK;
 }
 

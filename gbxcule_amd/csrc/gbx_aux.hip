@@ -284,12 +284,9 @@ __global__ __launch_bounds__(kFrameThreads) void frame_bg_kernel(DevState s, uin
   const uint32_t y = blockIdx.x;
   const uint32_t x = threadIdx.x;
   const Row r{s.mem, 0u};  // env 0: block 0, lane 0
-  const uint8_t* L = s.latches;
-  const uint32_t lcdc = L[0 * kScreenH + y], scx = L[1 * kScreenH + y];
-  const uint32_t scy = L[2 * kScreenH + y], bgp = L[3 * kScreenH + y];
-  const uint32_t wx = L[4 * kScreenH + y], wy = L[5 * kScreenH + y];
-  const uint32_t win_line = L[6 * kScreenH + y];
-  const uint32_t obp0 = L[7 * kScreenH + y], obp1 = L[8 * kScreenH + y];
+  const uint8_t* L = s.latches + (size_t)y * kLatchStride;
+  const uint32_t lcdc = L[0], scx = L[1], scy = L[2], bgp = L[3], wx = L[4], wy = L[5];
+  const uint32_t win_line = L[6], obp0 = L[7], obp1 = L[8];
   const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
   if (x < 64u) {
     bool on = false;
@@ -575,10 +572,11 @@ __global__ void env_image_kernel(DevState s, uint32_t env, uint8_t* img, int to_
     if (!to_device) img[kImgCram + off] = d;
     else if (parts & IMG_CRAM) d = img[kImgCram + off];
   } else if (i < n_mem + ram + (uint32_t)kLatchBytes) {
-    const uint32_t k = i - n_mem - ram;
+    const uint32_t k = i - n_mem - ram;  // [9][144] in the image
     uint8_t* src = img + img_latches_off((int)ram);
-    if (!to_device) src[k] = s.latches[k];
-    else if (parts & IMG_LATCHES) s.latches[k] = src[k];
+    uint8_t& d = s.latches[(k % (uint32_t)kScreenH) * kLatchStride + k / (uint32_t)kScreenH];
+    if (!to_device) src[k] = d;
+    else if (parts & IMG_LATCHES) d = src[k];
   }
 }
 

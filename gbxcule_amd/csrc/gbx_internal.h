@@ -10,6 +10,11 @@ namespace gbx {
 constexpr int kMemSize = 65536;
 constexpr int kEnvBlockShift = 6;  // 64 envs (one wavefront) per interleave block
 constexpr int kEnvBlock = 1 << kEnvBlockShift;
+// Env 0's scanline latches on the device, line-major: bytes LCDC, SCX, SCY,
+// BGP, WX, WY, window line, OBP0, OBP1 (then padding) of line y at
+// y * kLatchStride, written by one 16-byte store per line.  The C ABI and
+// the env image carry them as [9][144] (register-major).
+constexpr int kLatchStride = 16;
 constexpr int kSerialMax = 1024;
 constexpr int kCartStateStride = 20;
 constexpr int kScreenH = 144;
@@ -80,7 +85,7 @@ struct DevState {
   float* reward;        // [n]
   uint8_t* pix;         // [n][72][80]
   uint8_t* pix_packed;  // [n][72][20]
-  uint8_t* latches;     // [9][144] env-0 scanline latches
+  uint8_t* latches;     // [144][kLatchStride] env-0 scanline latches, one 16-byte entry per line
   uint8_t* frame_bg;    // [144][160] env-0 full-frame shades
   const uint8_t* rom;       // ROM image, the 256-byte boot image, 16 KiB of 0xFF (open bus)
   const uint8_t* boot;

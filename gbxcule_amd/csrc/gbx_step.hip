@@ -605,16 +605,11 @@ struct Lane {
   // the window line w, OBP0, OBP1.  `io` holds SCX | SCY << 8 | BGP << 16 |
   // WX << 24 and `obp` OBP0 | OBP1 << 8, as read from memory.
   __device__ void store_latches(uint32_t l, uint32_t w, uint32_t io, uint32_t obp) const {
-    uint8_t* Lt = s.latches;
-    Lt[0 * kScreenH + l] = (uint8_t)lcdc;
-    Lt[1 * kScreenH + l] = (uint8_t)io;
-    Lt[2 * kScreenH + l] = (uint8_t)(io >> 8);
-    Lt[3 * kScreenH + l] = (uint8_t)(io >> 16);
-    Lt[4 * kScreenH + l] = (uint8_t)(io >> 24);
-    Lt[5 * kScreenH + l] = (uint8_t)wy;
-    Lt[6 * kScreenH + l] = (uint8_t)(w & 0xFFu);
-    Lt[7 * kScreenH + l] = (uint8_t)obp;
-    Lt[8 * kScreenH + l] = (uint8_t)(obp >> 8);
+    // one 16-byte entry per line: LCDC SCX SCY BGP | WX WY WL OBP0 | OBP1
+    const uint4 v = make_uint4((lcdc & 0xFFu) | (io << 8), (io >> 24) | ((wy & 0xFFu) << 8) |
+                                                               ((w & 0xFFu) << 16) | (obp << 24),
+                               (obp >> 8) & 0xFFu, 0u);
+    *reinterpret_cast<uint4*>(s.latches + (size_t)l * kLatchStride) = v;
   }
   __device__ uint32_t latch_io() const {
     return (uint32_t)M(0xFF43) | ((uint32_t)M(0xFF42) << 8) | ((uint32_t)M(0xFF47) << 16) |
