@@ -90,6 +90,11 @@ struct Ref32 {
 };
 
 __device__ __forceinline__ uint32_t sel(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
+// Lane q's value of v, unsigned (the builtin returns int, which would
+// sign-extend when widened).
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t q) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)q);
+}
 
 // Launch-uniform values that the loop only uses in per-lane arithmetic (flat
 // base addresses, sizes, limits) are held in VGPRs: the loop body already
@@ -867,20 +872,6 @@ struct Lane {
     if ((hl >= 0x8000u) & (de > hl)) k = min(k, (int)(de - hl));
     return k;
   }
-  // The memory effect of k passes: bytes src..src+k-1 to dst..dst+k-1, in
-  // batches of eight loads then eight stores (windows as copy_passes checks).
-  __device__ void block_copy(uint32_t src, uint32_t dst, int k) {
-    const uint8_t* ps = bus_ptr(src);
-    const uint32_t ss = src < 0x8000u ? 1u : (uint32_t)kEnvBlock;
-    for (int j = 0; j < k; j += 8) {
-      uint32_t v[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] = (j + t < k) ? (uint32_t)ld_global(ps + (uint32_t)(j + t) * ss) : 0u;
-#pragma unroll
-      for (int t = 0; t < 8; ++t)
-        if (j + t < k) M(dst + (uint32_t)(j + t)) = v[t];
-    }
-  }
   // Cycles a step may take on the fast path: it must not reach a TIMA
   // edge, the scanline end or the frame end (0 while a switched-off LCD still
   // has PPU state to clear).
@@ -1052,6 +1043,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
     }
   };
 
+  // Block copies of the copy-loop fast-forward (bytes cp_src[j * cp_stride]
+  // to memory rows cp_dst + j of this lane's env, j < cp_k), done by every
+  // active lane of the wavefront together, one copying env after another:
+  // a lone lane would make one round trip per 8 bytes while the others
+  // wait.  copy_passes bounds k so that no byte is read after the same
+  // copy wrote it, so the bytes may be copied in any order.
+  uint32_t cp_k = 0, cp_dst = 0, cp_stride = 0;
+  const uint8_t* cp_src = nullptr;
+  auto coop_copy = [&]() {
+    const uint64_t act = __ballot(true);
+    uint64_t want = __ballot(cp_k != 0u);
+    const uint32_t me = __lane_id();
+    const uint32_t rank = (uint32_t)__popcll(act & ((1ull << me) - 1ull));
+    const uint32_t nact = (uint32_t)__popcll(act);
+    while (want) {
+      const uint32_t q = (uint32_t)__builtin_ctzll(want);
+      want &= want - 1u;
+      const uint32_t k = lane_value(cp_k, q);
+      const uint32_t dst = lane_value(cp_dst, q);
+      const uint32_t stride = lane_value(cp_stride, q);
+      const uint32_t ql = lane_value(L.lane, q);
+      const uint64_t sa = reinterpret_cast<uint64_t>(cp_src);
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(
+          ((uint64_t)lane_value((uint32_t)(sa >> 32), q) << 32) | (uint64_t)lane_value((uint32_t)sa, q));
+      for (uint32_t j = rank; j < k; j += 4u * nact) {
+        uint32_t v[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+          const uint32_t jx = j + t * nact;
+          v[t] = jx < k ? (uint32_t)ld_global(src + jx * stride) : 0u;
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+          const uint32_t jx = j + t * nact;
+          if (jx < k)
+            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)v[t], L.rm, (int)(((dst + jx) << kEnvBlockShift) | ql), 0, 0);
+        }
+      }
+    }
+  };
+
   // One exit: the frame count reached or the env trapped (a trap freezes
   // the env for the rest of the launch, misc.py:42-56).
   while ((L.frames_done < frames) & (trap == 0)) {
@@ -1121,55 +1153,67 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       wa1 = o.wa1;
       wv1 = o.wv1;
       uint32_t npc = o.npc;
-      if (__builtin_expect(o.misc != 0u, 0)) {  // DI EI RETI HALT, illegal opcodes, poll/copy loops
-        if (o.misc & 1u) {
-          L.ime = (o.misc >> 1) & 1u;
-          L.ime_delay = 0;
-        }
-        if (o.misc & 4u) L.halted = 1;
-        if (o.misc & 8u) {  // misc.py:42-56: freeze the env, pc unchanged
-          trap = 1;
-          trap_pc = (int)pc;
-          trap_op = (int)op;
-          trap_kind = 1;
-          L.budget = 0;
-        }
-        if (!dbg && (o.misc & 16u) && (rec.w[15] & kCopyLoop)) {
-          // LD A,(HL+) of a block-copy loop just ran: advance k whole passes
-          // (this LD included) in one step.  Each pass copies (HL+) to (DE)
-          // and steps DE and BC; OR leaves Z clear (BC stays non-zero), N,
-          // H and C clear, so F = 0 and A = B | C.
-          const uint32_t hl = in.w1 >> 16, de = in.w0 & 0xFFFFu, bc = in.w0 >> 16;
-          const int k = L.copy_passes(hl, de, bc, cframe);
-          if (k > 0) {
-            L.block_copy(hl, de, k);
-            const uint32_t nbc = (bc - (uint32_t)k) & 0xFFFFu;
-            L.w0 = (nbc << 16) | (de + (uint32_t)k);
-            L.w1 = ((hl + (uint32_t)k) << 16) | ((nbc | (nbc >> 8)) & 0xFFu);
-            npc = pc;
-            cycles = 52 * k;
-            ninstr += 7u * (uint32_t)k - 1u;
+      // (a wave-uniform test, so that the copy below runs with every lane
+      // that is executing an instruction)
+      if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0)) {
+        if (o.misc != 0u) {  // DI EI RETI HALT, illegal opcodes, poll/copy loops
+          if (o.misc & 1u) {
+            L.ime = (o.misc >> 1) & 1u;
+            L.ime_delay = 0;
           }
-        } else if (!dbg && (o.misc & 16u)) {
-          // LDH A,(44) just read LY into A; if CP d8 / JR cc takes the jump
-          // back, every pass until LY or anything else can change reads the
-          // same LY and leaves the same A and F: advance k whole passes (this
-          // LDH included) in one step.
-          const int k = L.poll_passes(rec.w[15], in.rd0, cframe);
-          if (k > 0) {
-            // A and F as the last pass's LDH and CP leave them
-            const uint32_t off = L.scan + 32u * (uint32_t)(k - 1);
-            const uint32_t ly = ((off < (uint32_t)kCyclesPerLine) | ((L.lcdc & 0x80u) == 0u))
-                                    ? in.rd0
-                                    : (L.ly + off / (uint32_t)kCyclesPerLine) % (uint32_t)kLinesPerFrame;
-            const uint32_t d8 = rec.w[15] & 0xFFu;
-            const uint32_t f = ((ly == d8) ? 0x80u : 0u) | 0x40u | (((ly & 15u) < (d8 & 15u)) ? 0x20u : 0u) |
-                               ((ly < d8) ? 0x10u : 0u);
-            L.w1 = (L.w1 & 0xFFFF0000u) | (f << 8) | ly;
-            npc = pc;
-            cycles = 32 * k;
-            ninstr += 3u * (uint32_t)k - 1u;
+          if (o.misc & 4u) L.halted = 1;
+          if (o.misc & 8u) {  // misc.py:42-56: freeze the env, pc unchanged
+            trap = 1;
+            trap_pc = (int)pc;
+            trap_op = (int)op;
+            trap_kind = 1;
+            L.budget = 0;
           }
+          if (!dbg && (o.misc & 16u) && (rec.w[15] & kCopyLoop)) {
+            // LD A,(HL+) of a block-copy loop just ran: advance k whole passes
+            // (this LD included) in one step.  Each pass copies (HL+) to (DE)
+            // and steps DE and BC; OR leaves Z clear (BC stays non-zero), N,
+            // H and C clear, so F = 0 and A = B | C.
+            const uint32_t hl = in.w1 >> 16, de = in.w0 & 0xFFFFu, bc = in.w0 >> 16;
+            const int k = L.copy_passes(hl, de, bc, cframe);
+            if (k > 0) {
+              // the k bytes are copied below by the whole wavefront
+              cp_k = (uint32_t)k;
+              cp_dst = de;
+              cp_src = L.bus_ptr(hl);
+              cp_stride = hl < 0x8000u ? 1u : (uint32_t)kEnvBlock;
+              const uint32_t nbc = (bc - (uint32_t)k) & 0xFFFFu;
+              L.w0 = (nbc << 16) | (de + (uint32_t)k);
+              L.w1 = ((hl + (uint32_t)k) << 16) | ((nbc | (nbc >> 8)) & 0xFFu);
+              npc = pc;
+              cycles = 52 * k;
+              ninstr += 7u * (uint32_t)k - 1u;
+            }
+          } else if (!dbg && (o.misc & 16u)) {
+            // LDH A,(44) just read LY into A; if CP d8 / JR cc takes the jump
+            // back, every pass until LY or anything else can change reads the
+            // same LY and leaves the same A and F: advance k whole passes (this
+            // LDH included) in one step.
+            const int k = L.poll_passes(rec.w[15], in.rd0, cframe);
+            if (k > 0) {
+              // A and F as the last pass's LDH and CP leave them
+              const uint32_t off = L.scan + 32u * (uint32_t)(k - 1);
+              const uint32_t ly = ((off < (uint32_t)kCyclesPerLine) | ((L.lcdc & 0x80u) == 0u))
+                                      ? in.rd0
+                                      : (L.ly + off / (uint32_t)kCyclesPerLine) % (uint32_t)kLinesPerFrame;
+              const uint32_t d8 = rec.w[15] & 0xFFu;
+              const uint32_t f = ((ly == d8) ? 0x80u : 0u) | 0x40u | (((ly & 15u) < (d8 & 15u)) ? 0x20u : 0u) |
+                                 ((ly < d8) ? 0x10u : 0u);
+              L.w1 = (L.w1 & 0xFFFF0000u) | (f << 8) | ly;
+              npc = pc;
+              cycles = 32 * k;
+              ninstr += 3u * (uint32_t)k - 1u;
+            }
+          }
+        }
+        if (!dbg && __ballot(cp_k != 0u) != 0u) {
+          coop_copy();
+          cp_k = 0;
         }
       }
       L.pc = npc;
