@@ -502,12 +502,21 @@ struct Lane {
       } break;
       case 0x46: {
         M(0xFF46) = v;
+        // 160 bytes, 4 loads in flight, then their stores.  Only a source
+        // page of FE overlaps the destination, and then batch b reads bytes
+        // FE00 + 4b .. that no earlier batch wrote, as the reference's
+        // byte-by-byte loop does.
         const uint32_t src = v << 8;
 #pragma unroll 1
-        for (uint32_t j = 0; j < 160; ++j) {
-          const uint32_t sa = (src + j) & 0xFFFFu;
-          const uint32_t b = M(sa);
-          M(0xFE00u + j) = io_derived(sa) ? io_fix(sa, b) : b;
+        for (uint32_t j0 = 0; j0 < 160; j0 += 4) {
+          uint32_t b[4];
+#pragma unroll
+          for (uint32_t t = 0; t < 4; ++t) b[t] = M((src + j0 + t) & 0xFFFFu);
+#pragma unroll
+          for (uint32_t t = 0; t < 4; ++t) {
+            const uint32_t sa = (src + j0 + t) & 0xFFFFu;
+            M(0xFE00u + j0 + t) = io_derived(sa) ? io_fix(sa, b[t]) : b[t];
+          }
         }
       } break;
       default:
