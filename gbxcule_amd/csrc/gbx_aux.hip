@@ -87,13 +87,17 @@ __device__ __forceinline__ uint32_t spread_tile(uint32_t t, uint32_t p) {
 // px = (x + s) & 0xFF (s = SCX for the background, 7 - WX for the window):
 // c[j] = the sampled colours (spread_tile) of map column ((s >> 3) + j) & 31.
 // Sample ox is then byte ox + ((s & 7) >> 1) of the byte stream c[0], c[1], ...
-// The 21 map reads are independent, then the 42 tile-data reads are.
-__device__ __forceinline__ void load_layer(const Row& r, uint32_t lcdc, uint32_t map, uint32_t s,
-                                           uint32_t py, uint32_t (&c)[kTileSlots]) {
+// The 21 map reads of a layer are independent (layer_ids), then its 42
+// tile-data reads are (layer_tiles); the caller issues both layers' map
+// reads before either layer's tile reads.
+__device__ __forceinline__ void layer_ids(const Row& r, uint32_t map, uint32_t s, uint32_t py,
+                                          uint32_t (&id)[kTileSlots]) {
   const uint32_t mrow = map + (py >> 3) * 32u;
-  uint32_t id[kTileSlots];
 #pragma unroll
   for (int j = 0; j < kTileSlots; ++j) id[j] = r.M(mrow + (((s >> 3) + (uint32_t)j) & 31u));
+}
+__device__ __forceinline__ void layer_tiles(const Row& r, uint32_t lcdc, uint32_t s, uint32_t py,
+                                            const uint32_t (&id)[kTileSlots], uint32_t (&c)[kTileSlots]) {
   const uint32_t row2 = (py & 7u) * 2u;
 #pragma unroll
   for (int j = 0; j < kTileSlots; ++j) {
@@ -166,41 +170,64 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
   for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&line[g][lane][0]) = make_uint2(0u, 0u);
   __syncthreads();
   if (lcdc & 0x02u) {
+    // OAM in batches of 8 entries: their LDS reads, then the tile-row loads
+    // of those on the line, then their pixels in OAM order
     uint32_t on_line = 0;
-    for (uint32_t k = 0; k < 40u && on_line < 10u; ++k) {
-      const uint32_t ent = oam[k][lane];
-      const uint32_t sy = ent & 0xFFu, sx = (ent >> 8) & 0xFFu;
-      if (sx == 0 || sy == 0 || sx >= 168u || sy >= 160u) continue;
-      const int top = (int)sy - 16;
-      if ((int)y < top || (int)y >= top + (int)height) continue;
-      ++on_line;
-      uint32_t tile = (ent >> 16) & 0xFFu;
-      const uint32_t attr = ent >> 24;
-      uint32_t row = (uint32_t)((int)y - top);
-      if ((attr >> 6) & 1u) row = height - 1u - row;
-      if (height == 16u) {
-        tile &= 0xFEu;
-        if (row >= 8u) {
-          tile += 1u;
-          row -= 8u;
+#pragma unroll 1
+    for (uint32_t k0 = 0; k0 < 40u; k0 += 8u) {
+      uint32_t ent[8], ta[8], lo[8], hi[8];
+      bool vis[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) ent[t] = oam[k0 + (uint32_t)t][lane];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t sy = ent[t] & 0xFFu, sx = (ent[t] >> 8) & 0xFFu;
+        const int top = (int)sy - 16;
+        vis[t] = (sx != 0u) & (sy != 0u) & (sx < 168u) & (sy < 160u) & ((int)y >= top) &
+                 ((int)y < top + (int)height) & (on_line < 10u);
+        on_line += vis[t] ? 1u : 0u;
+        uint32_t tile = (ent[t] >> 16) & 0xFFu;
+        const uint32_t attr = ent[t] >> 24;
+        uint32_t row = (uint32_t)((int)y - top) & 15u;
+        if ((attr >> 6) & 1u) row = (height - 1u - row) & 15u;
+        if (height == 16u) {
+          tile &= 0xFEu;
+          if (row >= 8u) {
+            tile += 1u;
+            row -= 8u;
+          }
         }
+        ta[t] = 0x8000u + tile * 16u + (row & 7u) * 2u;
       }
-      const uint32_t ta = 0x8000u + tile * 16u + row * 2u;
-      const uint32_t lo = r.M(ta), hi = r.M(ta + 1u);
-      const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
-      const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
-      const int left = (int)sx - 8;
-      // the sampled columns x = 2*ox inside [left, left + 8)
-      for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
-        if (x < 0 || x >= 2 * kDsW) continue;
-        const uint32_t pxl = (uint32_t)(x - left);
-        const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
-        const uint32_t color = (((hi >> bit) & 1u) << 1) | ((lo >> bit) & 1u);
-        if (color == 0) continue;
-        const uint32_t ox = (uint32_t)x >> 1;
-        uint16_t& slot = line[ox >> 2][lane][ox & 3u];
-        const uint32_t cur = slot;
-        if (cur == 0 || sx < (cur >> 8)) slot = (uint16_t)(tag | ((pal >> (color * 2u)) & 3u));
+      bool any = false;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) any |= vis[t];
+      if (__ballot(any) == 0u) continue;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        lo[t] = vis[t] ? r.M(ta[t]) : 0u;
+        hi[t] = vis[t] ? r.M(ta[t] + 1u) : 0u;
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if (!vis[t]) continue;
+        const uint32_t sx = (ent[t] >> 8) & 0xFFu;
+        const uint32_t attr = ent[t] >> 24;
+        const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
+        const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
+        const int left = (int)sx - 8;
+        // the sampled columns x = 2*ox inside [left, left + 8)
+        for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
+          if (x < 0 || x >= 2 * kDsW) continue;
+          const uint32_t pxl = (uint32_t)(x - left);
+          const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
+          const uint32_t color = (((hi[t] >> bit) & 1u) << 1) | ((lo[t] >> bit) & 1u);
+          if (color == 0) continue;
+          const uint32_t ox = (uint32_t)x >> 1;
+          uint16_t& slot = line[ox >> 2][lane][ox & 3u];
+          const uint32_t cur = slot;
+          if (cur == 0 || sx < (cur >> 8)) slot = (uint16_t)(tag | ((pal >> (color * 2u)) & 3u));
+        }
       }
     }
   }
@@ -214,10 +241,13 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
   for (int j = 0; j < kTileSlots; ++j) cb[j] = cw[j] = 0;
   if (bg_on) {
     // the background unless the window covers the whole row
-    if (!(win && wx7 <= 0))
-      load_layer(r, lcdc, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, (y + scy) & 0xFFu, cb);
-    if (win && wx7 < 2 * kDsW - 1)
-      load_layer(r, lcdc, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, (y - wy) & 0xFFu, cw);
+    const bool do_bg = !(win && wx7 <= 0), do_win = win && wx7 < 2 * kDsW - 1;
+    const uint32_t pyb = (y + scy) & 0xFFu, pyw = (y - wy) & 0xFFu;
+    uint32_t idb[kTileSlots], idw[kTileSlots];
+    if (do_bg) layer_ids(r, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, pyb, idb);
+    if (do_win) layer_ids(r, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, pyw, idw);
+    if (do_bg) layer_tiles(r, lcdc, scx, pyb, idb, cb);
+    if (do_win) layer_tiles(r, lcdc, sw, pyw, idw, cw);
   }
   const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
   // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
