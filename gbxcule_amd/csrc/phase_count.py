@@ -70,7 +70,7 @@ def marked_sources(dst: Path) -> None:
         "if (__builtin_expect((!plain_store(x0)) | (two & !plain_store(x1)), 0))",  # IO/MBC writes
         "if (__builtin_expect(!rv, 0))",  # fetch outside the record windows
         "if (__builtin_expect(nr > 1u, 0))",  # second read byte (POP, RET)
-        "if (__builtin_expect(o.misc != 0u, 0))",  # DI/EI/HALT/traps, poll and copy loops
+        "if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0))",  # DI/EI/HALT/traps, poll/copy loops
         "    } else {\n      cycles = L.halt_cycles(cframe);",  # halted lanes
         "    } else if (!trap) {\n      L.timer_tick(cycles);",  # full timer/PPU/IRQ sequence
     ):
