@@ -468,7 +468,8 @@ class HipVecBackend:
     def memory_blocks_torch(self):
         """Native zero-copy ``uint8 [ceil(N/64), 65536, 64]`` view: env ``e`` is
         ``[e // 64, :, e % 64]``.  Once it has been handed out, masked resets
-        also restore rows below 0x8000 (the view can write them)."""
+        also restore the rows the step never writes (below 0x8000, A000-BFFF,
+        E000-FDFF), since the view can write them."""
         npad = self._info(_lib.INFO_PADDED_ENVS)
         return self._view(_lib.BUF_MEM, (npad // ENV_BLOCK, MEM_SIZE, ENV_BLOCK), "uint8")
 

@@ -29,11 +29,13 @@ struct gbx_ctx {
   SnapState snap{};
   bool snap_valid = false;
   // Set once anything but the power-on fill may have written a memory row
-  // below 0x8000 (an import there, or the raw memory pointer handed out).
-  // The step never stores there (ROM-window writes go to the MBC), so while
-  // it is clear every env and the snapshot hold the power-on rows and a
-  // masked restore skips them.
-  bool low_rows_dirty = false;
+  // the step never writes: below 0x8000 (ROM-window writes go to the MBC),
+  // A000-BFFF (cartridge-RAM writes go to the cartridge RAM buffer) and
+  // E000-FDFF (echo writes fold to C000-DDFF).  Set by an import there, a
+  // gbx_write_mem there, or the raw memory pointer handed out.  While it is
+  // clear every env and the snapshot hold the power-on bytes in those rows,
+  // and a masked restore skips them.
+  bool dead_rows_dirty = false;
   std::vector<uint8_t> boot_host;  // the power-on fill of rows 0x00-0xFF
   uint64_t* hash_k = nullptr;
   int dbg[4] = {0, 0, 0, 0};
@@ -92,11 +94,14 @@ void* scratch_ptr(int dev) {
   return dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
 }
 
+// Rows of the memory image the step never writes.
+bool dead_row(int32_t a) { return a < 0x8000 || (a >= 0xA000 && a < 0xC000) || (a >= 0xE000 && a < 0xFE00); }
 // True when bytes [addr, addr + len) of an image differ from the power-on
-// fill (boot image at 0x00-0xFF, zero above) anywhere below 0x8000.
+// fill (boot image at 0x00-0xFF, zero elsewhere) in a dead row.
 bool differs_from_fill(const gbx_ctx* c, int32_t addr, const uint8_t* bytes, int32_t len) {
-  for (int32_t i = 0; i < len && addr + i < 0x8000; ++i) {
+  for (int32_t i = 0; i < len; ++i) {
     const int32_t a = addr + i;
+    if (!dead_row(a)) continue;
     const uint8_t fill = a < 0x100 ? c->boot_host[(size_t)a] : 0;
     if (bytes[i] != fill) return true;
   }
@@ -384,7 +389,7 @@ int gbx_masked_reset(gbx_ctx* ctx, const uint8_t* mask_dev, void* stream) {
   CHECK_CTX(ctx);
   if (!ctx->snap_valid) return fail(GBX_E_STATE, "no snapshot: call gbx_snapshot first");
   if (!mask_dev) return fail(GBX_E_INVALID, "mask is NULL");
-  HIP_TRY(launch_masked_reset(ctx->s, ctx->snap, mask_dev, ctx->low_rows_dirty ? 0 : 0x8000,
+  HIP_TRY(launch_masked_reset(ctx->s, ctx->snap, mask_dev, ctx->dead_rows_dirty ? 0 : 1,
                               (hipStream_t)stream));
   return GBX_OK;
 }
@@ -415,8 +420,8 @@ int gbx_write_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo, int3
   if (const int rc = check_rect(ctx, env_lo, env_hi, lo, hi)) return rc;
   if (env_lo == env_hi || lo == hi) return GBX_OK;
   if (!in_dev) return fail(GBX_E_INVALID, "in is NULL");
-  // the bytes are on the device: any write below 0x8000 may change those rows
-  if (lo < 0x8000) ctx->low_rows_dirty = true;
+  // the bytes are on the device: a write reaching a dead row may change it
+  if (lo < 0x8000 || (lo < 0xC000 && hi > 0xA000) || (lo < 0xFE00 && hi > 0xE000)) ctx->dead_rows_dirty = true;
   HIP_TRY(launch_mem_range(ctx->s, env_lo, env_hi - env_lo, lo, hi - lo,
                            const_cast<uint8_t*>(in_dev), 1, (hipStream_t)stream));
   return GBX_OK;
@@ -502,7 +507,7 @@ int gbx_import_mem(gbx_ctx* ctx, int32_t env, int32_t addr, const uint8_t* host_
   if (addr < 0 || len < 0 || addr > kMemSize || len > kMemSize - addr)
     return fail(GBX_E_INVALID, "write out of range");
   if (len == 0) return GBX_OK;
-  if (differs_from_fill(ctx, addr, host_in, len)) ctx->low_rows_dirty = true;
+  if (differs_from_fill(ctx, addr, host_in, len)) ctx->dead_rows_dirty = true;
   uint8_t* tmp = nullptr;
   HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMalloc(&tmp, (size_t)len));
@@ -633,8 +638,8 @@ int gbx_import_env(gbx_ctx* ctx, int32_t env, const int64_t* scalars, const int3
   CHECK_CTX(ctx);
   if (!scalars || !cart_state || !mem) return fail(GBX_E_INVALID, "in is NULL");
   if (env < 0 || env >= ctx->s.n) return fail(GBX_E_INVALID, "env out of range");
-  // rows below 0x8000 that still hold the power-on fill keep the flag clear
-  if (differs_from_fill(ctx, 0, mem, 0x8000)) ctx->low_rows_dirty = true;
+  // dead rows that still hold the power-on fill keep the flag clear
+  if (differs_from_fill(ctx, 0, mem, kMemSize)) ctx->dead_rows_dirty = true;
   const DevState& s = ctx->s;
   const size_t nb = img_bytes(s.ram_bytes);
   std::vector<uint8_t> h(nb, 0);
@@ -669,7 +674,7 @@ int gbx_buffer(gbx_ctx* ctx, int32_t which, void** dev_ptr, int64_t* nbytes) {
     case GBX_BUF_MEM:  // the caller may write any row through it
       *dev_ptr = s.mem;
       *nbytes = (int64_t)s.npad * kMemSize;
-      ctx->low_rows_dirty = true;
+      ctx->dead_rows_dirty = true;
       break;
     case GBX_BUF_PIX: *dev_ptr = s.pix; *nbytes = (int64_t)s.n * kDsW * kDsH; break;
     case GBX_BUF_PIX_PACKED: *dev_ptr = s.pix_packed; *nbytes = (int64_t)s.n * kDsWB * kDsH; break;

@@ -36,7 +36,7 @@ hipError_t launch_env_image(const DevState& s, int env, uint8_t* img, int to_dev
 hipError_t launch_snapshot(const DevState& s, const SnapState& snap, int env, int with_pix,
                            hipStream_t st);
 hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const uint8_t* mask,
-                               int first_row, hipStream_t st);
+                               int live, hipStream_t st);
 hipError_t launch_gather(const DevState& s, const uint16_t* addrs, int k, uint8_t* out,
                          hipStream_t st);
 hipError_t launch_hash(const DevState& s, const uint64_t* K, uint64_t* out, hipStream_t st);

@@ -415,14 +415,23 @@ __global__ void snapshot_kernel(DevState s, SnapState snap, uint32_t env, int wi
 // bytes, only when one of its bytes changed.  Every masked env of the block
 // is restored in the same pass, each row is read once, and no row is written
 // partially.  A workgroup of 256 threads covers kResetRows rows of one block,
-// four rows per thread in flight.  Rows below first_row are not restored
-// (the caller knows they already match).  Blocks without a masked env leave
-// at once.
+// four rows per thread in flight.  With `live` set only the rows the step
+// writes are restored (8000-9FFF, C000-DFFF, FE00-FFFF, then cartridge RAM):
+// the caller knows that the others still hold the power-on bytes in every
+// env and in the snapshot.  Blocks without a masked env leave at once.
 constexpr uint32_t kResetRows = 1024;
 constexpr int kResetBatch = 4;
+// Row of restore index i: every row of mem then of cartridge RAM, or with
+// `live` the live rows 8000-9FFF, C000-DFFF, FE00-FFFF then cartridge RAM.
+__device__ __forceinline__ uint32_t restore_row(uint32_t i, bool live) {
+  return !live ? i : i < 0x2000u ? 0x8000u + i : i < 0x4000u ? 0xA000u + i : 0xBE00u + i;
+}
+__host__ __device__ inline uint32_t restore_rows(uint32_t cram_stride, bool live) {
+  return (live ? 0x4200u : (uint32_t)kMemSize) + cram_stride;
+}
 __global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8_t* snap_mem,
                                                          const uint8_t* snap_cram, const uint8_t* mask,
-                                                         uint32_t first_row) {
+                                                         int live) {
   const uint32_t b = blockIdx.x, t = threadIdx.x;
   const uint32_t e = (b << kEnvBlockShift) | (t & (kEnvBlock - 1));
   const uint64_t bits = __ballot(e < (uint32_t)s.n && mask[e] != 0);
@@ -437,9 +446,9 @@ __global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8
     mw[j] = ((n4 & 1u) ? 0xFFu : 0u) | ((n4 & 2u) ? 0xFF00u : 0u) | ((n4 & 4u) ? 0xFF0000u : 0u) |
             ((n4 & 8u) ? 0xFF000000u : 0u);
   }
-  const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t r0 = first_row + blockIdx.y * kResetRows + (t >> 2);
-  const uint32_t r1 = min(per_env, first_row + (blockIdx.y + 1u) * kResetRows);
+  const uint32_t count = restore_rows((uint32_t)s.cram_stride, live != 0);
+  const uint32_t r0 = blockIdx.y * kResetRows + (t >> 2);
+  const uint32_t r1 = min(count, (blockIdx.y + 1u) * kResetRows);
   const size_t cram_base = (size_t)b * (size_t)s.cram_stride;
   for (uint32_t r = r0; r < r1; r += 64u * kResetBatch) {
     uint4* p[kResetBatch];
@@ -447,8 +456,9 @@ __global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8
     uint32_t w[kResetBatch];
 #pragma unroll
     for (int i = 0; i < kResetBatch; ++i) {
-      const uint32_t ri = r + 64u * (uint32_t)i;
-      const bool ok = ri < r1;
+      const uint32_t ii = r + 64u * (uint32_t)i;
+      const bool ok = ii < r1;
+      const uint32_t ri = restore_row(ii, live != 0);
       const bool in_mem = ri < (uint32_t)kMemSize;
       const uint32_t off = ri - (uint32_t)kMemSize;
       uint8_t* row = in_mem ? s.mem + ((size_t)b << 22) + ((size_t)ri << kEnvBlockShift)
@@ -651,12 +661,11 @@ hipError_t launch_snapshot(const DevState& s, const SnapState& snap, int env, in
 }
 
 hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const uint8_t* mask,
-                               int first_row, hipStream_t st) {
+                               int live, hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
-  const uint32_t per_env = (uint32_t)kMemSize + (uint32_t)s.cram_stride;
-  const uint32_t chunks = (per_env - (uint32_t)first_row + kResetRows - 1) / kResetRows;
+  const uint32_t chunks = (restore_rows((uint32_t)s.cram_stride, live != 0) + kResetRows - 1) / kResetRows;
   hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + kEnvBlock - 1) / kEnvBlock), chunks),
-                     dim3(256), 0, st, s, snap.mem, snap.cram, mask, (uint32_t)first_row);
+                     dim3(256), 0, st, s, snap.mem, snap.cram, mask, live);
   hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)s.n), dim3(256), 0, st, s, snap, mask,
                      snap.has_pix);
   return hipGetLastError();

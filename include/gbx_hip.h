@@ -55,7 +55,8 @@ enum { GBX_STAGE_EMULATE_ONLY = 0, GBX_STAGE_REWARD_ONLY = 1,
 /* Buffers exposed for zero-copy views (gbx_buffer). */
 enum {
   GBX_BUF_MEM = 0,        /* u8, 64-env blocks: [(N+63)/64][65536][64]; once handed out,
-                            gbx_masked_reset also restores rows below 0x8000
+                            gbx_masked_reset also restores the rows the step never
+                            writes (below 0x8000, A000-BFFF, E000-FDFF)
                             (gbx_read_mem / gbx_write_mem reach memory without it) */
   GBX_BUF_PIX = 1,        /* u8 [N][72][80] unpacked 2-bit shades */
   GBX_BUF_PIX_PACKED = 2, /* u8 [N][72][20] packed, 4 shades per byte */
@@ -137,8 +138,8 @@ int gbx_read_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo,
 /* The reverse: in_dev (same env-major layout) into the rectangle.  Writes
  * through the reference's memory_torch() view (mem[:, 0xFF40] |= 0x80,
  * the LCDC override of backends/warp_vec.py:734-757) land here.  A write
- * with lo < 0x8000 makes gbx_masked_reset restore rows below 0x8000 from
- * then on. */
+ * that reaches a row the step never writes (below 0x8000, A000-BFFF,
+ * E000-FDFF) makes gbx_masked_reset restore those rows from then on. */
 int gbx_write_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo,
                   int32_t hi, const uint8_t* in_dev, void* stream);
 
@@ -153,9 +154,10 @@ int gbx_export_scalar(gbx_ctx* ctx, int32_t field, int64_t* host_out);
 int gbx_import_scalar(gbx_ctx* ctx, int32_t field, const int64_t* host_in);
 int gbx_export_mem(gbx_ctx* ctx, int32_t env_lo, int32_t env_hi, int32_t lo,
                    int32_t hi, uint8_t* host_out);
-/* gbx_import_mem and gbx_import_env write rows below 0x8000 only as data:
- * while every such row still holds the power-on fill (boot image at
- * 0x00-0xFF, zero above), gbx_masked_reset keeps skipping them. */
+/* gbx_import_mem and gbx_import_env write the rows the step never writes
+ * (below 0x8000, A000-BFFF, E000-FDFF) only as data: while every such row
+ * still holds the power-on fill (boot image at 0x00-0xFF, zero elsewhere),
+ * gbx_masked_reset keeps skipping them. */
 int gbx_import_mem(gbx_ctx* ctx, int32_t env, int32_t addr,
                    const uint8_t* host_in, int32_t len);
 int gbx_export_cart_state(gbx_ctx* ctx, int32_t* host_out);

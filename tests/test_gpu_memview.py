@@ -81,7 +81,9 @@ def test_reference_indexing_matches_export(carts, bootstub):
 
 def dma_cart() -> bytes:
     """ROM-only cart that, every frame, runs OAM DMA from page 0x00 (the boot
-    image rows of memory) then from page 0x01, and copies OAM bytes to WRAM."""
+    image rows of memory), page 0x01, page 0xA0 (cartridge-RAM rows, which a
+    cart without RAM never writes) and page 0xE1 (echo rows, whose writes fold
+    to work RAM), and copies OAM bytes to WRAM."""
     a = Asm(origin=PROGRAM_ORIGIN)
     a.ld_rr_d16("SP", 0xDFF0)
     a.ld_r_d8("A", 0x91)
@@ -91,16 +93,16 @@ def dma_cart() -> bytes:
     a.ldh_a_a8(0x44)
     a.alu_d8("CP", 144)
     a.jr("w1", "NZ")
-    for page in (0x00, 0x01):
+    for i, page in enumerate((0x00, 0x01, 0xA0, 0xE1)):
         a.ld_r_d8("A", page)
         a.ldh_a8_a(0x46)
         a.ld_r_d8("A", 0xFF)  # a few cycles between transfers
-        a.label(f"w{page + 2}")
+        a.label(f"w{i + 2}")
         a.ldh_a_a8(0x44)
-        a.alu_d8("CP", 145 + page)
-        a.jr(f"w{page + 2}", "NZ")
-        a.ld_a_a16(0xFE00 + 3 * page)
-        a.ld_a16_a(0xC000 + page)
+        a.alu_d8("CP", 145 + i)
+        a.jr(f"w{i + 2}", "NZ")
+        a.ld_a_a16(0xFE00 + 3 * i)
+        a.ld_a16_a(0xC000 + i)
     a.jp("loop")
     rom = bytearray(0x8000)
     _vectors(rom)
@@ -109,8 +111,23 @@ def dma_cart() -> bytes:
     return finalize_rom(rom, "DMALOW", 0x00, 0x00, 0x00)
 
 
-@pytest.mark.parametrize("route", ["load_state", "load_state_low_rows", "memory_torch", "memory_blocks_torch"])
-def test_low_rows_restored_exactly_when_changed(bootstub, route):
+@pytest.mark.parametrize(
+    "route",
+    [
+        "load_state",
+        "load_state_low_rows",
+        "load_state_cart_ram_rows",
+        "load_state_echo_rows",
+        "memory_torch",
+        "memory_torch_cart_ram_rows",
+        "memory_torch_echo_rows",
+        "memory_blocks_torch",
+    ],
+)
+def test_dead_rows_restored_exactly_when_changed(bootstub, route):
+    """Rows the step never writes (below 0x8000, A000-BFFF, E000-FDFF) are
+    skipped by masked resets until a route may have changed them; every route
+    that can must make the restore cover them again."""
     require_gpu()
     import torch
 
@@ -135,11 +152,16 @@ def test_low_rows_restored_exactly_when_changed(bootstub, route):
             np.testing.assert_array_equal(img.mem, ref_export_env(ref, 9).mem)
             if route == "load_state_low_rows":
                 img.mem[0x00:0x40] ^= 0xA5  # boot-image rows, read by the page-0 DMA
+            elif route == "load_state_cart_ram_rows":
+                img.mem[0xA000:0xA040] ^= 0x5A  # read by the page-0xA0 DMA
+            elif route == "load_state_echo_rows":
+                img.mem[0xE100:0xE140] ^= 0x3C  # read by the page-0xE1 DMA
             dut.import_env(5, img)
             ref_import_env(ref, 5, img)
-        elif route == "memory_torch":
-            dut.memory_torch()[5, 0x0010:0x0020] = 0x77
-            ref.mem[5, 0x0010:0x0020] = 0x77
+        elif route.startswith("memory_torch"):
+            lo = {"memory_torch": 0x0010, "memory_torch_cart_ram_rows": 0xA010, "memory_torch_echo_rows": 0xE110}[route]
+            dut.memory_torch()[5, lo : lo + 0x10] = 0x77
+            ref.mem[5, lo : lo + 0x10] = 0x77
         else:
             blocks = dut.memory_blocks_torch()
             blocks[0, 0x0030, 5] = 0x66
@@ -151,7 +173,7 @@ def test_low_rows_restored_exactly_when_changed(bootstub, route):
         cache.apply_mask_torch(torch.from_numpy(mask).cuda().bool())
         ref.masked_reset(mask)
         assert_same_state(dut, ref, step=3, tag=f"{route} restore")
-        for k in range(3, 6):  # the DMA reads rows 0x0000-0x019F of every env
+        for k in range(3, 6):  # the DMAs read rows 0x0000-0x019F, 0xA000-0xA09F, 0xE100-0xE19F
             act = seeded_actions(7, k, n)
             dut.step(act)
             ref.step(act, fs, 8, "full_step")
