@@ -153,6 +153,11 @@ struct Lane {
   uint32_t sp0;         // ppu_stat_prev as loaded (until the first PPU step)
   uint32_t lyc_pp;      // LYC at the last PPU step
   uint32_t lcd_pp;      // LCDC bit 7 at the last PPU step; 0x100 before the first
+  // Set when the fast path may run through quiet scanline changes (those
+  // that raise no request) without applying them: scan then exceeds a line
+  // (settle_lines).  Never for env 0, whose latches need every line, nor in
+  // the debug variants.
+  uint32_t defer;
   // cartridge
   uint32_t boot_en;
   uint32_t rom_lo, rom_hi;  // byte offset of the 0000 / 4000 windows in the ROM buffer
@@ -284,7 +289,9 @@ struct Lane {
       v = (cart & !ram_ok) ? 0xFFu : v;  // no RTC: disabled RAM reads 0xFF
     }
     v = x == 0xFF04u ? ff04_val() : v;
-    if (__builtin_expect(x == 0xFF41u, 0)) v = stat_val();
+    // STAT, and LY while scanline changes are deferred (FF44 holds the LY
+    // of the last applied change)
+    if (__builtin_expect((x & 0xFFFAu) == 0xFF40u, 0)) v = read_ppu(x, v);
     return v;
   }
   __device__ uint32_t read8(uint32_t addr) const {
@@ -437,6 +444,7 @@ struct Lane {
     return (x >= 0xFF00u) & ((k == 0xFFu) | (((m >> (k & 31u)) & 1u) != 0u));
   }
   __device__ void io_write(uint32_t x, uint32_t v) {
+    settle_lines();  // the write follows every change the fast path deferred
     budget = 0;  // timer, LCD and PPU registers feed event_budget
     const uint32_t k = x & 0xFFu;
     // plain register copies
@@ -649,9 +657,33 @@ struct Lane {
       if (l < (uint32_t)kScreenH) store_latches(l, w, io, obp);
     }
   }
-  // STAT mode of the current position (LCD on)
-  __device__ uint32_t mode_now(uint32_t sc) const {
-    return ly >= (uint32_t)kScreenH ? 1u : sc < 80u ? 2u : sc < 250u ? 3u : 0u;
+  // STAT mode at scanline cycle sc of line l (LCD on)
+  __device__ static uint32_t mode_at(uint32_t l, uint32_t sc) {
+    return l >= (uint32_t)kScreenH ? 1u : sc < 80u ? 2u : sc < 250u ? 3u : 0u;
+  }
+  __device__ uint32_t mode_now(uint32_t sc) const { return mode_at(ly, sc); }
+  // The line m changes (m < 154) after line ly.
+  __device__ uint32_t line_after(uint32_t m) const {
+    const uint32_t l = ly + m;
+    return l >= (uint32_t)kLinesPerFrame ? l - (uint32_t)kLinesPerFrame : l;
+  }
+  // Applies the scanline changes the fast path deferred (scan >= 456).  None
+  // of them raises a request (event_budget stops short of every change that
+  // can), so they change only LY, the window line and FF44, and applying
+  // them together gives what applying them one at a time gives.  Everything
+  // that observes the PPU position calls this first, except LY and STAT
+  // reads, which derive their values (read_ppu).
+  __device__ void settle_lines() {
+    if (scan < (uint32_t)kCyclesPerLine) return;
+    advance_lines(scan / (uint32_t)kCyclesPerLine);
+    M(0xFF44) = lym;
+  }
+  // FF40, FF41, FF44 and FF45 as the bus reads them: STAT from the PPU
+  // position, LY after the deferred changes, the others as stored.
+  __device__ uint32_t read_ppu(uint32_t x, uint32_t v) const {
+    const uint32_t m = scan / (uint32_t)kCyclesPerLine;
+    v = ((x == 0xFF44u) & (m != 0u)) ? line_after(m) : v;
+    return x == 0xFF41u ? stat_val() : v;
   }
   __device__ static uint32_t stat_bits(uint32_t mode, uint32_t coin) {
     return (mode == 0 ? 1u : 0u) | (mode == 1 ? 2u : 0u) | (mode == 2 ? 4u : 0u) | (coin << 3);
@@ -661,8 +693,11 @@ struct Lane {
   // derived here from that position instead of being stored per step.
   __device__ uint32_t stat_val() const {
     if (stat_fresh) return stat_full;
-    const uint32_t coin = ly == lyc_pp ? 1u : 0u;
-    return (stat_full & 0xF8u) | (coin << 2) | (lcd_pp ? mode_now(scan) : 0u);
+    // the position after any deferred scanline changes
+    const uint32_t m = scan / (uint32_t)kCyclesPerLine;
+    const uint32_t l = line_after(m), sc = scan - m * (uint32_t)kCyclesPerLine;
+    const uint32_t coin = l == lyc_pp ? 1u : 0u;
+    return (stat_full & 0xF8u) | (coin << 2) | (lcd_pp ? mode_at(l, sc) : 0u);
   }
   // ppu_stat_prev as the reference holds it after the last PPU step that
   // ended at scanline cycle sc.
@@ -737,15 +772,21 @@ struct Lane {
                       (((en & 1u) != 0u) & (j0 >= 2u) & (j0 <= m)) |
                       (((en & 8u) != 0u) & (jl >= 2u) & (jl <= m));
     ifr |= ((uint32_t)stat << 1) | (uint32_t)(j144 <= m);
-    uint32_t lf = ly + m;  // <= 307
-    lf = lf >= nl ? lf - nl : lf;
-    const bool wrapped = j0 <= m;
+    advance_lines(m);
+  }
+  // LY, the window line and the scanline position after m line changes
+  // (1 <= m <= 154) from line ly < 154, with LCDC and WY fixed over them:
+  // the window line counter counts the lines left below 144 and at or past
+  // WY (LCDC bit 5), restarting at 0 when line 0 is entered, which happens
+  // iff ly + m reaches 154.
+  __device__ void advance_lines(uint32_t m) {
+    const uint32_t lf = line_after(m);
     // lines in [a, b) below 144 and at or past WY, with the window on
     auto counted = [&](uint32_t a, uint32_t b) {
       const int hi = min((int)b, kScreenH), lo = max((int)a, (int)wy);
       return (lcdc & 0x20u) && hi > lo ? (uint32_t)(hi - lo) : 0u;
     };
-    wl = wrapped ? counted(0u, lf) : wl + counted(ly, lf);
+    wl = ly + m >= (uint32_t)kLinesPerFrame ? counted(0u, lf) : wl + counted(ly, lf);
     ly = lf;
     lym = lf;
     scan -= m * (uint32_t)kCyclesPerLine;
@@ -888,7 +929,14 @@ struct Lane {
     int b = kCyclesPerFrame - cframe;
     const uint32_t te = tmask - (div & 0xFFFFu & tmask);
     b = te < (uint32_t)b ? (int)te + 1 : b;
-    b = (lcdc & 0x80u) ? min(b, kCyclesPerLine - (int)scan) : ((scan | ly | wl | lym) != 0u ? 0 : b);
+    // the scanline end, or with deferral the end of the first change that
+    // can raise a request: into line 144 (VBlank, STAT mode 1) or into line
+    // LYC with the LYC source on.  With the HBlank source on every change
+    // can (its request compares with the STAT bits where the previous
+    // instruction ended).
+    const bool lazy = (defer != 0u) & ((stat_full & 0x08u) == 0u);
+    b = (lcdc & 0x80u) ? min(b, lazy ? line_horizon(3u) : kCyclesPerLine - (int)scan)
+                       : ((scan | ly | wl | lym) != 0u ? 0 : b);
     if ((mbc == MBC_MBC3) & (rtc_halt == 0u))  // the next RTC second
       b = ((rtc_dirty != 0u) | (rtc_sub < 0)) ? 0 : min(b, kRtcCyclesPerSecond - rtc_sub);
     // a pending TIMA reload, EI delay, interrupt request or bank remap takes
@@ -946,6 +994,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
   Lane L{s};
   L.mbc = kMbc;
   L.e = e;
+  L.defer = (!kDbg && e != 0u) ? 1u : 0u;
   L.lane = e & (kEnvBlock - 1);
   const uint32_t blk = __builtin_amdgcn_readfirstlane(e >> kEnvBlockShift);
   L.rm = make_rsrc(s.mem + ((size_t)blk << 22), 1u << 22);
@@ -1166,6 +1215,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       // that is executing an instruction)
       if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0)) {
         if (o.misc != 0u) {  // DI EI RETI HALT, illegal opcodes, poll/copy loops
+          L.settle_lines();  // the fast-forwards start from the PPU position
           if (o.misc & 1u) {
             L.ime = (o.misc >> 1) & 1u;
             L.ime_delay = 0;
@@ -1230,6 +1280,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       load_rec(L.next_rec(npc, rv));
       }
     } else {
+      L.settle_lines();
       cycles = L.halt_cycles(cframe);
     }
 
@@ -1274,6 +1325,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       cframe += cycles;
       L.budget -= cycles;
     } else if (!trap) {
+      L.settle_lines();
       L.timer_tick(cycles);
       if (!hiter & (L.ime_delay != 0u)) {
         L.ime = 1;
@@ -1351,6 +1403,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
       L.budget = L.event_budget(cframe);
     }
   }
+  L.settle_lines();
   instr += ninstr;
   cyc += ncyc;
 
