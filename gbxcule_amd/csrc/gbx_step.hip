@@ -627,9 +627,13 @@ struct Lane {
   // the window line w, OBP0, OBP1.  `io` holds SCX | SCY << 8 | BGP << 16 |
   // WX << 24 and `obp` OBP0 | OBP1 << 8, as read from memory.
   __device__ void store_latches(uint32_t l, uint32_t w, uint32_t io, uint32_t obp) const {
+    store_latch_entry(l, w, lcdc, wy, io, obp);
+  }
+  __device__ void store_latch_entry(uint32_t l, uint32_t w, uint32_t lc, uint32_t wyv, uint32_t io,
+                                    uint32_t obp) const {
     // one 16-byte entry per line: LCDC SCX SCY BGP | WX WY WL OBP0 | OBP1
-    const uint4 v = make_uint4((lcdc & 0xFFu) | (io << 8), (io >> 24) | ((wy & 0xFFu) << 8) |
-                                                               ((w & 0xFFu) << 16) | (obp << 24),
+    const uint4 v = make_uint4((lc & 0xFFu) | (io << 8), (io >> 24) | ((wyv & 0xFFu) << 8) |
+                                                             ((w & 0xFFu) << 16) | (obp << 24),
                                (obp >> 8) & 0xFFu, 0u);
     *reinterpret_cast<uint4*>(s.latches + (size_t)l * kLatchStride) = v;
   }
@@ -643,18 +647,31 @@ struct Lane {
     store_latches(ly, wl, latch_io(), latch_obp());
   }
   // Env 0's latches for the visible lines entered by a run of m line
-  // changes from line ly (the run's registers are fixed: no IO write falls
-  // between the lines of one step, so they are read once), with the window
-  // line counter as each change leaves it.
-  __device__ void latch_run(uint32_t m) const {
-    const uint32_t io = latch_io(), obp = latch_obp();
-    const bool win = (lcdc & 0x20u) != 0u;
-    uint32_t l = ly, w = wl;
-    for (uint32_t j = 0; j < m; ++j) {
-      w += (uint32_t)((l < (uint32_t)kScreenH) & win & (l >= wy));
-      l = l + 1u == (uint32_t)kLinesPerFrame ? 0u : l + 1u;
-      w = l == 0u ? 0u : w;
-      if (l < (uint32_t)kScreenH) store_latches(l, w, io, obp);
+  // changes (2 <= m <= 154) from line ly.  The run's registers are fixed (no
+  // IO write falls between the lines of one step), so they are read once.
+  // Each entry has a closed form: change j enters line l = (ly + j + 1) % 154,
+  // once each, and leaves the window line counter at wl plus the lines in
+  // [ly, l) below 144 and at or past WY (window on), or at the lines in
+  // [0, l) once the run has entered line 0.  So every active lane of env 0's
+  // wavefront writes a share of the entries; env 0 is lane 0, whose values
+  // the others read.  Called by all active lanes when one of them is env 0.
+  __device__ void latch_run_wave(uint32_t m) const {
+    const auto rl0 = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readlane((int)x, 0); };
+    const uint32_t io = rl0(latch_io()), obp = rl0(latch_obp());
+    const uint32_t m0 = rl0(m), l0 = rl0(ly), w0 = rl0(wl), lc = rl0(lcdc), wy0 = rl0(wy);
+    const uint64_t act = __ballot(true);
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(act >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)act, 0u));
+    const uint32_t nact = (uint32_t)__popcll(act);
+    auto counted = [&](uint32_t a, uint32_t b) {
+      const int hi = min((int)b, kScreenH), lo = max((int)a, (int)wy0);
+      return (lc & 0x20u) && hi > lo ? (uint32_t)(hi - lo) : 0u;
+    };
+    for (uint32_t j = rank; j < m0; j += nact) {
+      const uint32_t t = l0 + j + 1u;  // <= 307
+      const bool wrapped = t >= (uint32_t)kLinesPerFrame;
+      const uint32_t l = wrapped ? t - (uint32_t)kLinesPerFrame : t;
+      const uint32_t w = wrapped ? counted(0u, l) : w0 + counted(l0, l);
+      if (l < (uint32_t)kScreenH) store_latch_entry(l, w, lc, wy0, io, obp);
     }
   }
   // STAT mode at scanline cycle sc of line l (LCD on)
@@ -710,13 +727,13 @@ struct Lane {
   // The reference applies each change in turn (cpu_step_builder.py:1436-
   // 1480).  A run of m >= 2 changes, the batched steps of a halted CPU, an LY
   // poll or a block copy, is applied in closed form (ppu_lines_run), after
-  // env 0 has recorded the run's scanline latches (latch_run).
+  // env 0 has recorded the run's scanline latches (latch_run_wave).
   __device__ void ppu_lines(uint32_t s0) {
     uint32_t prev = stat_prev_at(s0);
     // (the run test is one compare; C2-like code never takes it)
     if (__builtin_expect(scan >= 2u * (uint32_t)kCyclesPerLine, 0)) {
       const uint32_t m = scan / (uint32_t)kCyclesPerLine;
-      if (e == 0u) latch_run(m);
+      if (__builtin_expect(__ballot(e == 0u) != 0u, 0)) latch_run_wave(m);
       ppu_lines_run(m, prev);
     } else {
       const uint32_t lc = lcdc;
@@ -988,7 +1005,7 @@ struct Lane {
 // One variant per cartridge kind (kMbc) and per debug mode (kDbg): the
 // cartridge code of other kinds and every debug check compile out.
 template <int kMbc, bool kDbg>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void step_kernel(DevState s, StepArgs args) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void step_kernel(DevState s, StepArgs args) {
   const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (uint32_t)s.n) return;
   Lane L{s};
@@ -1490,9 +1507,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void st
 
 hipError_t launch_step(const DevState& s, const StepArgs& a, hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
-  // One wavefront per workgroup carrying step_lanes envs (a divisor of the
-  // 64-env memory block, so a wavefront never straddles two blocks).
-  const int threads = s.step_lanes;
+  // A wavefront carries step_lanes envs (a divisor of the 64-env memory
+  // block, so it never straddles two blocks).  Full 64-lane wavefronts go
+  // four to a workgroup: the four land on the four SIMDs of one CU, where
+  // single-wavefront workgroups left some SIMDs with three wavefronts and
+  // others with one (the wavefronts on a crowded SIMD set the launch time).
+  // Narrower wavefronts (few envs) stay one to a workgroup, one per SIMD.
+  const int threads = s.step_lanes == kEnvBlock ? 4 * kEnvBlock : s.step_lanes;
   const int blocks = (s.n + threads - 1) / threads;
   const bool dbg = a.dbg_rst38 || a.dbg_trap_pc || a.dbg_max_instr > 0 || a.dbg_watch;
   const dim3 g(blocks), b(threads);
