@@ -131,61 +131,90 @@ __device__ __forceinline__ void store_rows(const uint32_t* stage, uint8_t* rows,
 
 // One workgroup per 64-env memory block and 4 output rows; lanes are the
 // block's envs, so every read of one address by a wavefront is one 64-byte
-// row.  The block's OAM is staged into LDS once for the 4 rows.  Per row, the
-// sprites (the first 10 OAM entries overlapping the line, counted before the
-// x test) are resolved into a line buffer of the 80 samples: each sample
-// keeps the opaque sprite pixel with the lowest x (ties: the lower OAM index,
-// the earlier entry), as the reference's per-sample search over OAM selects
-// it.  The BG and window tile rows are fetched for all 21 tile columns at
-// once; the samples are then shaded four at a time, one per byte: the
-// group's colours are a byte window of the layer's colour stream, the window
-// layer is blended in by a byte mask, BGP maps colours to shades through a
-// byte permute, and the sprite overlay is a byte mask.
+// row.  The block's OAM is staged into LDS once for the 4 rows, and with it,
+// per entry and row, whether the entry covers the row (position valid, row
+// inside its 8 or 16 lines).  Per row, the sprites (the first 10 OAM
+// entries covering the line, counted before the x test) are resolved into a
+// line buffer of the 80 samples: each sample keeps the opaque sprite pixel
+// with the lowest x (ties: the lower OAM index, the earlier entry), as the
+// reference's per-sample search over OAM selects it.  A lane walks only its
+// own covering entries, in OAM order, two per round.  The BG and window tile
+// rows are fetched for all 21 tile columns at once; the samples are then
+// shaded four at a time, one per byte: the group's colours are a byte window
+// of the layer's colour stream, the window layer is blended in by a byte
+// mask, BGP maps colours to shades through a byte permute, and the sprite
+// overlay is a byte mask.
 __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
                                                                 int packed) {
   // OAM entry k of each env: y | x << 8 | tile << 16 | attr << 24
   __shared__ uint32_t oam[40][kEnvBlock];
+  // entries 10w .. 10w + 9 (staged by wavefront w) covering row r: bit i
+  __shared__ uint16_t cover[kRenderRows][kRenderRows][kEnvBlock];
   // sprite line buffer per row, 4 samples per (group, lane): 0 = no sprite
   // pixel, else bits [0:1] its shade (palette applied), [2] behind non-zero
   // BG, [3] set, [8:15] the sprite's OAM x (its left edge + 8)
   __shared__ __align__(16) uint16_t obj[kRenderRows][kGroups][kEnvBlock][4];
+  static_assert(kRenderRows * 10 == 40, "each wavefront stages 10 OAM entries");
   const uint32_t lane = threadIdx.x & (kEnvBlock - 1);
   const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> kEnvBlockShift);
   const uint32_t blk = blockIdx.x;
   const Row r{s.mem + ((size_t)blk << 22), lane};  // the block's spare lanes render but never store
+  const uint32_t lcdc = r.M(0xFF40);
+  const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
+  const uint32_t y0 = blockIdx.y * kRenderRows * 2u;  // screen row of the workgroup's first output row
+  {
+    uint32_t cv[kRenderRows] = {};
 #pragma unroll
-  for (int i = 0; i < 40 / kRenderRows; ++i) {
-    const uint32_t k = wv + (uint32_t)(kRenderRows * i);
-    const uint32_t a = 0xFE00u + 4u * k;
-    oam[k][lane] = r.M(a) | (r.M(a + 1u) << 8) | (r.M(a + 2u) << 16) | (r.M(a + 3u) << 24);
+    for (uint32_t i = 0; i < 10u; ++i) {
+      const uint32_t k = 10u * wv + i;
+      const uint32_t a = 0xFE00u + 4u * k;
+      const uint32_t sy = r.M(a), sx = r.M(a + 1u);
+      oam[k][lane] = sy | (sx << 8) | (r.M(a + 2u) << 16) | (r.M(a + 3u) << 24);
+      const bool valid = (sx != 0u) & (sy != 0u) & (sx < 168u) & (sy < 160u);
+#pragma unroll
+      for (int q = 0; q < kRenderRows; ++q)  // row y0 + 2q inside [sy - 16, sy - 16 + height)
+        cv[q] |= (uint32_t)(valid & (y0 + 2u * (uint32_t)q + 16u - sy < height)) << i;
+    }
+#pragma unroll
+    for (int q = 0; q < kRenderRows; ++q) cover[q][wv][lane] = (uint16_t)cv[q];
   }
   const uint32_t oy = blockIdx.y * kRenderRows + wv;
   const uint32_t y = oy * 2u;
-  const uint32_t lcdc = r.M(0xFF40), scy = r.M(0xFF42), scx = r.M(0xFF43);
+  const uint32_t scy = r.M(0xFF42), scx = r.M(0xFF43);
   const uint32_t bgp = r.M(0xFF47), obp0 = r.M(0xFF48), obp1 = r.M(0xFF49);
   const uint32_t wy = r.M(0xFF4A), wx = r.M(0xFF4B);
-  const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
   uint16_t (&line)[kGroups][kEnvBlock][4] = obj[wv];
 #pragma unroll
   for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&line[g][lane][0]) = make_uint2(0u, 0u);
   __syncthreads();
   if (lcdc & 0x02u) {
-    // OAM in batches of 8 entries: their LDS reads, then the tile-row loads
-    // of those on the line, then their pixels in OAM order
-    uint32_t on_line = 0;
+    // the entries covering this row in OAM order, then only the first 10
+    uint64_t vis = 0;
+#pragma unroll
+    for (int w = 0; w < kRenderRows; ++w) vis |= (uint64_t)cover[wv][w][lane] << (10 * w);
+    if (__builtin_expect(__ballot(__popcll(vis) > 10) != 0u, 0)) {
+      uint64_t rest = vis;
+#pragma unroll
+      for (int j = 0; j < 10; ++j) rest &= rest - 1u;  // clears the lowest 10
+      vis &= ~rest;
+    }
+    // each lane's covering entries, lowest OAM index first, two per round
+    // (their tile-row loads issued together)
 #pragma unroll 1
-    for (uint32_t k0 = 0; k0 < 40u; k0 += 8u) {
-      uint32_t ent[8], ta[8], lo[8], hi[8];
-      bool vis[8];
+    while (__ballot(vis != 0u) != 0u) {
+      uint32_t ent[2], lo[2], hi[2];
+      bool on[2];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) ent[t] = oam[k0 + (uint32_t)t][lane];
+      for (int t = 0; t < 2; ++t) {
+        on[t] = vis != 0u;
+        const uint32_t k = on[t] ? (uint32_t)__builtin_ctzll(vis) : 0u;
+        vis &= vis - 1u;
+        ent[t] = oam[k][lane];
+      }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const uint32_t sy = ent[t] & 0xFFu, sx = (ent[t] >> 8) & 0xFFu;
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t sy = ent[t] & 0xFFu;
         const int top = (int)sy - 16;
-        vis[t] = (sx != 0u) & (sy != 0u) & (sx < 168u) & (sy < 160u) & ((int)y >= top) &
-                 ((int)y < top + (int)height) & (on_line < 10u);
-        on_line += vis[t] ? 1u : 0u;
         uint32_t tile = (ent[t] >> 16) & 0xFFu;
         const uint32_t attr = ent[t] >> 24;
         uint32_t row = (uint32_t)((int)y - top) & 15u;
@@ -197,20 +226,13 @@ __global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint
             row -= 8u;
           }
         }
-        ta[t] = 0x8000u + tile * 16u + (row & 7u) * 2u;
-      }
-      bool any = false;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) any |= vis[t];
-      if (__ballot(any) == 0u) continue;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        lo[t] = vis[t] ? r.M(ta[t]) : 0u;
-        hi[t] = vis[t] ? r.M(ta[t] + 1u) : 0u;
+        const uint32_t ta = 0x8000u + tile * 16u + (row & 7u) * 2u;
+        lo[t] = on[t] ? r.M(ta) : 0u;
+        hi[t] = on[t] ? r.M(ta + 1u) : 0u;
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        if (!vis[t]) continue;
+      for (int t = 0; t < 2; ++t) {
+        if (!on[t]) continue;
         const uint32_t sx = (ent[t] >> 8) & 0xFFu;
         const uint32_t attr = ent[t] >> 24;
         const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;

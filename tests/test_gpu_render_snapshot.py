@@ -34,7 +34,7 @@ def _scene(rng: np.random.Generator) -> dict[int, bytes]:
     return {0x8000: vram.tobytes(), 0xFE00: oam.tobytes(), 0xFF40: io.tobytes()}
 
 
-@pytest.mark.parametrize("n,seed", [(200, 5), (64, 6)])
+@pytest.mark.parametrize("n,seed", [(200, 5), (64, 6), (256, 7)])
 def test_snapshot_render_random_scenes(carts, bootstub, n, seed):
     require_gpu()
     import torch
