@@ -146,6 +146,9 @@ struct Lane {
   // timer
   uint32_t div, pend, delay;
   uint32_t tmask;       // no TIMA edge while (div & tmask) + cycles <= tmask
+  // DIV when TIMA was last brought up to date: the fast path may run through
+  // TIMA edges short of an overflow without applying them (settle_timer)
+  uint32_t tdiv;
   uint32_t tp_w;        // DIV or TAC written this launch
   uint32_t ff04_0, tprev0;  // FF04 and timer_prev_in as loaded
   // PPU
@@ -158,6 +161,7 @@ struct Lane {
   // (settle_lines).  Never for env 0, whose latches need every line, nor in
   // the debug variants.
   uint32_t defer;
+  uint32_t defer_timer;  // the same for TIMA edges (any env; not in debug variants)
   // cartridge
   uint32_t boot_en;
   uint32_t rom_lo, rom_hi;  // byte offset of the 0000 / 4000 windows in the ROM buffer
@@ -288,10 +292,10 @@ struct Lane {
     } else {
       v = (cart & !ram_ok) ? 0xFFu : v;  // no RTC: disabled RAM reads 0xFF
     }
-    v = x == 0xFF04u ? ff04_val() : v;
-    // STAT, and LY while scanline changes are deferred (FF44 holds the LY
-    // of the last applied change)
-    if (__builtin_expect((x & 0xFFFAu) == 0xFF40u, 0)) v = read_ppu(x, v);
+    // DIV and STAT, which follow from the timer and PPU position, and TIMA and
+    // LY while edges and scanline changes are deferred (FF05 and FF44 hold
+    // the values of the last applied ones): FF04 FF05 FF40 FF41 FF44 FF45
+    if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) v = read_ppu(x, v);
     return v;
   }
   __device__ uint32_t read8(uint32_t addr) const {
@@ -373,6 +377,9 @@ struct Lane {
       M(0xFF0F) = ifr;
     }
     div = d;
+    // TIMA holds every edge up to here, so a settle later in the same step
+    // (an IO write by an interrupt's push) counts none of them again
+    tdiv = d;
   }
 
   // -- MBC3 real-time clock (cpu_step_builder.py:374-419) ----------------------
@@ -444,7 +451,7 @@ struct Lane {
     return (x >= 0xFF00u) & ((k == 0xFFu) | (((m >> (k & 31u)) & 1u) != 0u));
   }
   __device__ void io_write(uint32_t x, uint32_t v) {
-    settle_lines();  // the write follows every change the fast path deferred
+    settle();  // the write follows every change and edge the fast path deferred
     budget = 0;  // timer, LCD and PPU registers feed event_budget
     const uint32_t k = x & 0xFFu;
     // plain register copies
@@ -530,6 +537,7 @@ struct Lane {
       default:
         break;
     }
+    tdiv = div;  // a DIV or TAC write starts the count afresh
   }
   __device__ void mbc_write(uint32_t x, uint32_t v) {
     const int kind = mbc;
@@ -695,11 +703,35 @@ struct Lane {
     advance_lines(scan / (uint32_t)kCyclesPerLine);
     M(0xFF44) = lym;
   }
-  // FF40, FF41, FF44 and FF45 as the bus reads them: STAT from the PPU
-  // position, LY after the deferred changes, the others as stored.
+  // TIMA edges the fast path ran through since DIV was tdiv (none overflows:
+  // event_budget stops at the overflowing edge), counted as timer_tick
+  // counts several edges in one step.
+  __device__ uint32_t tima_edges() const {
+    const uint32_t c = (div - tdiv) & 0xFFFFu;  // the budget keeps it below 65536
+    return (tac & 4u) ? ((tdiv & tmask) + c) >> (div_bit(tac) + 1u) : 0u;
+  }
+  __device__ void settle_timer() {
+    const uint32_t n = tima_edges();
+    if (n != 0u) {
+      tima += n;
+      M(0xFF05) = tima;
+    }
+    tdiv = div;
+  }
+  // Deferred scanline changes and TIMA edges, applied before anything that
+  // observes them other than the reads read_ppu derives.
+  __device__ void settle() {
+    settle_lines();
+    settle_timer();
+  }
+  // FF04, FF05, FF40, FF41, FF44 and FF45 as the bus reads them: DIV from
+  // the counter, TIMA after the deferred edges, STAT from the PPU position,
+  // LY after the deferred changes, the others as stored.
   __device__ uint32_t read_ppu(uint32_t x, uint32_t v) const {
     const uint32_t m = scan / (uint32_t)kCyclesPerLine;
     v = ((x == 0xFF44u) & (m != 0u)) ? line_after(m) : v;
+    v = x == 0xFF05u ? tima + tima_edges() : v;
+    v = x == 0xFF04u ? ff04_val() : v;
     return x == 0xFF41u ? stat_val() : v;
   }
   __device__ static uint32_t stat_bits(uint32_t mode, uint32_t coin) {
@@ -945,7 +977,12 @@ struct Lane {
   __device__ int event_budget(int cframe) const {
     int b = kCyclesPerFrame - cframe;
     const uint32_t te = tmask - (div & 0xFFFFu & tmask);
-    b = te < (uint32_t)b ? (int)te + 1 : b;
+    // the next TIMA edge, or with deferral the edge that overflows TIMA
+    // (at most 65,535 cycles on, so the DIV difference stays exact)
+    const uint32_t tov = ((defer_timer != 0u) & ((tac & 4u) != 0u))
+                             ? min(te + 1u + (0xFFu - (tima & 0xFFu)) * (tmask + 1u), 0xFFFFu)
+                             : te + 1u;
+    b = tov < (uint32_t)b ? (int)tov : b;
     // the scanline end, or with deferral the end of the first change that
     // can raise a request: into line 144 (VBlank, STAT mode 1) or into line
     // LYC with the LYC source on.  With the HBlank source on every change
@@ -1012,6 +1049,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   L.mbc = kMbc;
   L.e = e;
   L.defer = (!kDbg && e != 0u) ? 1u : 0u;
+  L.defer_timer = kDbg ? 0u : 1u;
   L.lane = e & (kEnvBlock - 1);
   const uint32_t blk = __builtin_amdgcn_readfirstlane(e >> kEnvBlockShift);
   L.rm = make_rsrc(s.mem + ((size_t)blk << 22), 1u << 22);
@@ -1049,6 +1087,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   L.tma = L.M(0xFF06);
   L.tac = L.M(0xFF07);
   L.tmask = Lane::edge_mask(L.tac);
+  L.tdiv = L.div;
   L.ifr = L.M(0xFF0F);
   L.lcdc = L.M(0xFF40);
   L.stat_full = L.M(0xFF41);
@@ -1232,7 +1271,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       // that is executing an instruction)
       if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0)) {
         if (o.misc != 0u) {  // DI EI RETI HALT, illegal opcodes, poll/copy loops
-          L.settle_lines();  // the fast-forwards start from the PPU position
+          L.settle();  // the fast-forwards start from the PPU and timer state
           if (o.misc & 1u) {
             L.ime = (o.misc >> 1) & 1u;
             L.ime_delay = 0;
@@ -1297,7 +1336,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       load_rec(L.next_rec(npc, rv));
       }
     } else {
-      L.settle_lines();
+      L.settle();
       cycles = L.halt_cycles(cframe);
     }
 
@@ -1342,7 +1381,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       cframe += cycles;
       L.budget -= cycles;
     } else if (!trap) {
-      L.settle_lines();
+      L.settle();
       L.timer_tick(cycles);
       if (!hiter & (L.ime_delay != 0u)) {
         L.ime = 1;
@@ -1420,7 +1459,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       L.budget = L.event_budget(cframe);
     }
   }
-  L.settle_lines();
+  L.settle();
   instr += ninstr;
   cyc += ncyc;
 

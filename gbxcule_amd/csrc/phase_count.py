@@ -63,16 +63,16 @@ def marked_sources(dst: Path) -> None:
     step = _insert(step, "    const uint32_t lc_now = L.lcdc;", m("tail"))
     step = _insert(step, "      L.budget -= cycles;\n", m("loop"), after=True)
     step = _insert(step, "  instr += ninstr;\n  cyc += ncyc;\n\n  // ---- post-step", m("exit"))
-    step = step.replace("if (__builtin_expect((x & 0xFFFAu) == 0xFF40u, 0)) v = read_ppu(x, v);",
-                        "if (__builtin_expect((x & 0xFFFAu) == 0xFF40u, 0)) { v = read_ppu(x, v); }")
+    step = step.replace("if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) v = read_ppu(x, v);",
+                        "if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) { v = read_ppu(x, v); }")
     for anchor in (
-        "if (__builtin_expect((x & 0xFFFAu) == 0xFF40u, 0))",  # STAT and deferred-LY read fix-up
+        "if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0))",  # STAT and deferred-LY read fix-up
         "if (__builtin_expect((!plain_store(x0)) | (two & !plain_store(x1)), 0))",  # IO/MBC writes
         "if (__builtin_expect(!rv, 0))",  # fetch outside the record windows
         "if (__builtin_expect(nr > 1u, 0))",  # second read byte (POP, RET)
         "if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0))",  # DI/EI/HALT/traps, poll/copy loops
-        "    } else {\n      L.settle_lines();\n      cycles = L.halt_cycles(cframe);",  # halted lanes
-        "    } else if (!trap) {\n      L.settle_lines();\n      L.timer_tick(cycles);",  # full timer/PPU/IRQ sequence
+        "    } else {\n      L.settle();\n      cycles = L.halt_cycles(cframe);",  # halted lanes
+        "    } else if (!trap) {\n      L.settle();\n      L.timer_tick(cycles);",  # full timer/PPU/IRQ sequence
     ):
         step = _rare(step, anchor)
     exe = (CSRC / "gbx_exec.h").read_text()
@@ -183,7 +183,7 @@ def main() -> int:
             tot[k] += c.get(k, 0)
         L.append(f"| {LABELS[p]} | " + " | ".join(str(c.get(k, 0)) for k in cols) + f" | {sum(c.values())} |")
     L.append("| **one loop iteration** | " + " | ".join(f"**{tot[k]}**" for k in cols) + f" | **{sum(tot.values())}** |")
-    L += ["", "Rare blocks (skipped when no lane runs them): STAT/LY read fix-up, IO/MBC writes, fetch outside the "
+    L += ["", "Rare blocks (skipped when no lane runs them): DIV/TIMA/STAT/LY read fix-up, IO/MBC writes, fetch outside the "
           "record windows, the second read byte, DI/EI/HALT/trap and poll/copy fast-forward, halted lanes, the full "
           "timer/PPU/interrupt sequence, DAA."]
     text = "\n".join(L) + "\n"

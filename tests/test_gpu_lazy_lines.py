@@ -1,17 +1,18 @@
-"""Scanline changes that raise no request, run through by the fast path,
-against the oracle.
+"""Scanline changes that raise no request and TIMA edges short of an
+overflow, run through by the fast path, against the oracle.
 
 Between the steps that can raise a request (the change into line 144, into
 line LYC with the LYC STAT source on, every change with the HBlank source
-on), the step kernel lets plain instructions run through scanline changes
-without applying them, and LY and STAT reads derive their values from the
-position.  These carts spend their time in delay loops of seeded, joypad-
-dependent lengths and read LY and STAT through LDH, LD A,(C) and LD A,(HL)
-at whatever position the loop ends, folding each byte into work RAM.
-Interrupt handlers read both registers too and move LYC; the window is on
-in some carts (its line counter is part of the compared state), one cart
-writes LY, and env 0 (which applies every change) shares a wavefront with
-envs that defer.  State is compared in full after every step.
+on, the TIMA overflow), the step kernel lets plain instructions run through
+scanline changes and TIMA edges without applying them, and LY, STAT, TIMA
+and DIV reads derive their values.  These carts spend their time in delay
+loops of seeded, joypad-dependent lengths and read LY, STAT, TIMA and DIV
+through LDH, LD A,(C) and LD A,(HL) at whatever position the loop ends,
+folding each byte into work RAM.  Interrupt handlers read LY and STAT too
+and move LYC; the window is on in some carts (its line counter is part of
+the compared state), some carts write LY, DIV, TIMA and TAC, the timer runs
+at every rate, and env 0 (which applies every scanline change) shares a
+wavefront with envs that defer.  State is compared in full after every step.
 """
 
 from __future__ import annotations
@@ -29,7 +30,8 @@ from .conftest import require_gpu
 pytestmark = pytest.mark.gpu
 
 
-def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, ly_write: bool) -> bytes:
+def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, ly_write: bool,
+              timer_writes: bool = False) -> bytes:
     rng = np.random.default_rng(seed)
     rom = bytearray(0x8000)
     h = Asm(origin=0x0068)
@@ -94,17 +96,21 @@ def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, 
         a.label(f"d{i}")
         a.dec_r("B")
         a.jr(f"d{i}", "NZ")
-        kind = i % 4
+        kind = i % 6
         if kind == 0:
             a.ldh_a_a8(0x44)
         elif kind == 1:
             a.ldh_a_a8(0x41)
         elif kind == 2:
-            a.ld_r_d8("C", 0x44 if i % 8 == 2 else 0x41)
+            a.ld_r_d8("C", (0x44, 0x05)[i // 6] if i < 12 else 0x41)
             a.emit(0xF2)  # LD A,(C)
-        else:
-            a.ld_rr_d16("HL", 0xFF44 if i % 8 == 3 else 0xFF41)
+        elif kind == 3:
+            a.ld_rr_d16("HL", (0xFF41, 0xFF04)[i // 6])
             a.emit(0x7E)  # LD A,(HL)
+        elif kind == 4:
+            a.ldh_a_a8(0x05)  # TIMA
+        else:
+            a.ldh_a_a8(0x04)  # DIV
         a.ld_rr_d16("HL", 0xC000 + i)
         a.alu_r("ADD", "(HL)")
         a.emit(0x77)  # LD (HL),A
@@ -113,6 +119,18 @@ def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, 
             a.ldh_a8_a(0x44)  # the next change overwrites it
             a.ldh_a_a8(0x44)
             a.ld_a16_a(0xC010)
+        if timer_writes and i in (3, 7, 10):
+            if i == 3:
+                a.ldh_a8_a(0x04)  # DIV reset
+            elif i == 7:
+                a.ld_r_d8("A", int(rng.integers(0, 256)))
+                a.ldh_a8_a(0x05)  # TIMA
+            else:
+                a.ldh_a_a8(0x07)
+                a.alu_d8("XOR", 0x01)  # another rate
+                a.ldh_a8_a(0x07)
+            a.ldh_a_a8(0x05)
+            a.ld_a16_a(0xC011 + i)
     a.jp("loop")
     code = a.resolve()
     rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
@@ -120,23 +138,28 @@ def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, 
 
 
 CASES = [
-    # seed, IME, IE, TAC, STAT sources (HBlank 0x08, VBlank 0x10, OAM 0x20, LYC 0x40), window, LY write
-    (1, True, 0x03, 0x00, 0x40, True, False),
-    (2, True, 0x01, 0x05, 0x10, False, False),
-    (3, False, 0x00, 0x00, 0x00, True, False),
-    (4, True, 0x02, 0x00, 0x08, False, False),
-    (5, True, 0x07, 0x04, 0x60, True, False),
-    (6, False, 0x02, 0x06, 0x50, False, True),
-    (7, True, 0x06, 0x07, 0x20, True, True),
+    # seed, IME, IE, TAC, STAT sources (HBlank 0x08, VBlank 0x10, OAM 0x20, LYC 0x40), window, LY write,
+    # DIV/TIMA/TAC writes
+    (1, True, 0x03, 0x00, 0x40, True, False, False),
+    (2, True, 0x01, 0x05, 0x10, False, False, False),
+    (3, False, 0x00, 0x00, 0x00, True, False, False),
+    (4, True, 0x02, 0x00, 0x08, False, False, False),
+    (5, True, 0x07, 0x04, 0x60, True, False, False),
+    (6, False, 0x02, 0x06, 0x50, False, True, False),
+    (7, True, 0x06, 0x07, 0x20, True, True, False),
+    (8, True, 0x04, 0x05, 0x00, False, False, True),
+    (9, False, 0x04, 0x06, 0x40, True, False, True),
+    (10, True, 0x05, 0x07, 0x10, False, True, True),
+    (11, True, 0x07, 0x04, 0x08, True, False, True),
 ]
 
 
-@pytest.mark.parametrize("seed,ime,ie,tac,stat,window,ly_write", CASES)
-def test_lazy_scanline_parity(bootstub, seed, ime, ie, tac, stat, window, ly_write):
+@pytest.mark.parametrize("seed,ime,ie,tac,stat,window,ly_write,timer_writes", CASES)
+def test_lazy_scanline_parity(bootstub, seed, ime, ie, tac, stat, window, ly_write, timer_writes):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
 
-    rom = lazy_cart(seed, ime, ie, tac, stat, window, ly_write)
+    rom = lazy_cart(seed, ime, ie, tac, stat, window, ly_write, timer_writes)
     n, fs, steps = 128, 6, 4
     dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=3,
                         stage="emulate_only", bootrom=bootstub)  # fmt: skip
@@ -158,6 +181,8 @@ def test_lazy_scanline_parity(bootstub, seed, ime, ie, tac, stat, window, ly_wri
             assert int(mem[1, 0xDF00]) > 0  # VBlank interrupts were serviced
         if ime and ie & 2 and stat & 0x48:
             assert int(mem[1, 0xDF01]) > 0  # STAT interrupts were serviced
+        if ime and ie & 4 and tac & 4:
+            assert int(mem[1, 0xDF02]) > 0  # timer interrupts were serviced
         assert int(ref.field("trap_flag").sum()) == 0
     finally:
         dut.close()
