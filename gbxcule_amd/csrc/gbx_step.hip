@@ -603,30 +603,31 @@ struct Lane {
     else write_special(x, v);
   }
   // Addresses a write reaches as a plain byte store without side effects:
-  // video RAM, work RAM, high RAM (FF80-FFFE), and FF00, whose store is the
-  // joypad value for the written select bits.  Everything else (ROM/MBC
-  // registers, cartridge RAM, echo RAM, OAM, IO registers, IE) goes through
-  // write8.  x is a 16-bit address.
-  __device__ static bool plain_store(uint32_t x) {
-    return (((0x3300u >> (x >> 12)) & 1u) != 0u) | (x - 0xFF80u < 0x7Fu) | (x == 0xFF00u);
+  // video RAM, work RAM and high RAM (FF80-FFFE) (plain_ram), and for the
+  // first byte of a write also FF00, whose store is the joypad value for the
+  // written select bits.  Everything else (ROM/MBC registers, cartridge RAM,
+  // echo RAM, OAM, IO registers, IE, and FF00 as a second byte, which only a
+  // push or LD (a16),SP next to it makes) goes through write8.  x is a
+  // 16-bit address.
+  __device__ static bool plain_ram(uint32_t x) {
+    return (((0x3300u >> (x >> 12)) & 1u) != 0u) | (x - 0xFF80u < 0x7Fu);
   }
+  __device__ static bool plain_store(uint32_t x) { return plain_ram(x) | (x == 0xFF00u); }
   // The instruction's bus writes, in order (n = 0, 1 or 2).  When both are
   // plain stores they are stored without a branch; a lane with one write
   // stores its first byte twice.
   __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1) {
     const uint32_t x0 = a0 & 0xFFFFu, x1 = a1 & 0xFFFFu;
     const bool two = n >= 2u;
-    if (__builtin_expect((!plain_store(x0)) | (two & !plain_store(x1)), 0)) {
+    if (__builtin_expect((!plain_store(x0)) | (two & !plain_ram(x1)), 0)) {
       write8(a0, v0);
       if (two) write8(a1, v1);
     } else {
-      const bool j0 = x0 == 0xFF00u, j1 = two & (x1 == 0xFF00u);
+      const bool j0 = x0 == 0xFF00u;
       const uint32_t s0 = j0 ? joyp_read(v0) : v0;
-      const uint32_t s1 = two ? (j1 ? joyp_read(v1) : v1) : s0;
       joyp_sel = j0 ? v0 & 0x30u : joyp_sel;
-      joyp_sel = j1 ? v1 & 0x30u : joyp_sel;
       M(x0) = s0;
-      M(two ? x1 : x0) = s1;
+      M(two ? x1 : x0) = two ? v1 : s0;
     }
   }
 
@@ -1233,13 +1234,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
 
       // ---- bus reads ------------------------------------------------------------
       const uint32_t nr = ubfe(rec.w[7], 8, 2);
-      in.rd0 = 0;
-      in.rd1 = 0;
-      if (nr) {
-        // A second load only for two-byte reads (POP, RET), issued before
-        // either byte is used; that byte sits one address row (64 bytes)
-        // after the first when both are in the env's memory.  A lane with
-        // one read repeats its first byte.
+      {
+        // Every lane loads the byte at its operand address, reading or not
+        // (a read has no side effect, and the folded address is always on
+        // the bus): no branch around the load, which lets it issue as early
+        // as its address allows.  A second load only for two-byte reads
+        // (POP, RET), issued before either byte is used; that byte sits one
+        // address row (64 bytes) after the first when both are in the env's
+        // memory.  A lane with one read repeats its first byte.
         const uint32_t x0 = Lane::fold(in.ra);
         const uint8_t* p0 = L.bus_ptr(x0);
         const uint32_t v0 = ld_global(p0);
@@ -1251,7 +1253,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
             p1 = L.bus_ptr(x1);
           v1 = ld_global(p1);
         }
-        in.rd0 = L.bus_fix(x0, v0);
+        in.rd0 = nr != 0u ? L.bus_fix(x0, v0) : 0u;
         in.rd1 = nr > 1u ? L.bus_fix(x1, v1) : in.rd0;
       }
 

@@ -67,7 +67,7 @@ def marked_sources(dst: Path) -> None:
                         "if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) { v = read_ppu(x, v); }")
     for anchor in (
         "if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0))",  # STAT and deferred-LY read fix-up
-        "if (__builtin_expect((!plain_store(x0)) | (two & !plain_store(x1)), 0))",  # IO/MBC writes
+        "if (__builtin_expect((!plain_store(x0)) | (two & !plain_ram(x1)), 0))",  # IO/MBC writes
         "if (__builtin_expect(!rv, 0))",  # fetch outside the record windows
         "if (__builtin_expect(nr > 1u, 0))",  # second read byte (POP, RET)
         "if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0))",  # DI/EI/HALT/traps, poll/copy loops
