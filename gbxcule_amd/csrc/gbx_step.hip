@@ -295,7 +295,8 @@ struct Lane {
     // DIV and STAT, which follow from the timer and PPU position, and TIMA and
     // LY while edges and scanline changes are deferred (FF05 and FF44 hold
     // the values of the last applied ones): FF04 FF05 FF40 FF41 FF44 FF45
-    if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) v = read_ppu(x, v);
+    const bool fx = ((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u);
+    if (__builtin_expect(__ballot(fx) != 0u, 0)) v = fx ? read_ppu(x, v) : v;
     return v;
   }
   __device__ uint32_t read8(uint32_t addr) const {
@@ -1213,9 +1214,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
     if (__builtin_expect(!hiter, 1)) {
       // ---- fetch + decode ------------------------------------------------------
       const uint32_t pc = L.pc;
-      if (__builtin_expect(!rv, 0)) {
-        if (L.rec_ok(pc)) load_rec(L.rec_index(pc));
-        else rec = L.fetch_slow();
+      // (rare branches of the per-instruction path test a wave-uniform
+      // ballot first: when no lane takes them the path keeps its exec mask
+      // instead of saving and restoring it around a skipped block)
+      if (__builtin_expect(__ballot(!rv) != 0u, 0)) {
+        if (!rv) {
+          if (L.rec_ok(pc)) load_rec(L.rec_index(pc));
+          else rec = L.fetch_slow();
+        }
       }
       op = rec.w[0] & 0xFFu;
       if (dbg) {  // debug traps before execution: the instruction does not run

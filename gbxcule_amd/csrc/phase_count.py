@@ -63,12 +63,12 @@ def marked_sources(dst: Path) -> None:
     step = _insert(step, "    const uint32_t lc_now = L.lcdc;", m("tail"))
     step = _insert(step, "      L.budget -= cycles;\n", m("loop"), after=True)
     step = _insert(step, "  instr += ninstr;\n  cyc += ncyc;\n\n  // ---- post-step", m("exit"))
-    step = step.replace("if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) v = read_ppu(x, v);",
-                        "if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0)) { v = read_ppu(x, v); }")
+    step = step.replace("if (__builtin_expect(__ballot(fx) != 0u, 0)) v = fx ? read_ppu(x, v) : v;",
+                        "if (__builtin_expect(__ballot(fx) != 0u, 0)) { v = fx ? read_ppu(x, v) : v; }")
     for anchor in (
-        "if (__builtin_expect(((x & 0xFFBAu) == 0xFF00u) & (x > 0xFF01u), 0))",  # STAT and deferred-LY read fix-up
+        "if (__builtin_expect(__ballot(fx) != 0u, 0))",  # STAT and deferred-LY read fix-up
         "if (__builtin_expect((!plain_store(x0)) | (two & !plain_ram(x1)), 0))",  # IO/MBC writes
-        "if (__builtin_expect(!rv, 0))",  # fetch outside the record windows
+        "if (__builtin_expect(__ballot(!rv) != 0u, 0))",  # fetch outside the record windows
         "if (__builtin_expect(nr > 1u, 0))",  # second read byte (POP, RET)
         "if (__builtin_expect(__ballot(o.misc != 0u) != 0u, 0))",  # DI/EI/HALT/traps, poll/copy loops
         "    } else {\n      L.settle();\n      cycles = L.halt_cycles(cframe);",  # halted lanes
