@@ -127,6 +127,7 @@ __device__ __forceinline__ T ld_global(const T* p) {
 struct Lane {
   const DevState& s;
   int mbc;        // cartridge kind; a compile-time constant of each kernel variant
+  bool cram;      // the cart declares RAM; compile-time too (ROM-only carts may)
   uint32_t e;     // env index
   uint32_t lane;  // e % 64: position inside the 64-env block
   rsrc_t rm, rsc, rcs;             // memory image, scalars, cartridge state of the block
@@ -265,8 +266,10 @@ struct Lane {
     const bool bootw = (boot_en != 0u) & (x < 0x100u);
     const uint32_t win = (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
     const uint32_t roff = win + ((rom_len + x - win) & (0u - (uint32_t)bootw));
-    const uint32_t coff = (mbc == MBC_ROM_ONLY || !ram_ok) ? lane
-                          : ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane;
+    // (a ROM-only cart without RAM never has ram_ok: its offset folds away)
+    const uint32_t coff = ((mbc == MBC_ROM_ONLY) & !cram) | !ram_ok
+                              ? lane
+                              : ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane;
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
     p = cart ? cramb + coff : p;
     p = rom ? this->rom + roff : p;
@@ -1041,14 +1044,16 @@ struct Lane {
 // ---------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------
-// One variant per cartridge kind (kMbc) and per debug mode (kDbg): the
-// cartridge code of other kinds and every debug check compile out.
-template <int kMbc, bool kDbg>
+// One variant per cartridge kind (kMbc), per debug mode (kDbg) and, for
+// ROM-only carts, per declared RAM (kCram): the cartridge code of other
+// kinds and every debug check compile out.
+template <int kMbc, bool kDbg, bool kCram = true>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void step_kernel(DevState s, StepArgs args) {
   const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (uint32_t)s.n) return;
   Lane L{s};
   L.mbc = kMbc;
+  L.cram = kCram;
   L.e = e;
   L.defer = (!kDbg && e != 0u) ? 1u : 0u;
   L.defer_timer = kDbg ? 0u : 1u;
@@ -1564,9 +1569,16 @@ hipError_t launch_step(const DevState& s, const StepArgs& a, hipStream_t st) {
   const int blocks = (s.n + threads - 1) / threads;
   const bool dbg = a.dbg_rst38 || a.dbg_trap_pc || a.dbg_max_instr > 0 || a.dbg_watch;
   const dim3 g(blocks), b(threads);
+  const bool rom_ram = s.mbc_kind == MBC_ROM_ONLY && s.ram_banks > 0;
   switch (s.mbc_kind * 2 + (dbg ? 1 : 0)) {
-    case MBC_ROM_ONLY * 2: hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, false>), g, b, 0, st, s, a); break;
-    case MBC_ROM_ONLY * 2 + 1: hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, true>), g, b, 0, st, s, a); break;
+    case MBC_ROM_ONLY * 2:
+      if (rom_ram) hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, false, true>), g, b, 0, st, s, a);
+      else hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, false, false>), g, b, 0, st, s, a);
+      break;
+    case MBC_ROM_ONLY * 2 + 1:
+      if (rom_ram) hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, true, true>), g, b, 0, st, s, a);
+      else hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, true, false>), g, b, 0, st, s, a);
+      break;
     case MBC_MBC1 * 2: hipLaunchKernelGGL((step_kernel<MBC_MBC1, false>), g, b, 0, st, s, a); break;
     case MBC_MBC1 * 2 + 1: hipLaunchKernelGGL((step_kernel<MBC_MBC1, true>), g, b, 0, st, s, a); break;
     case MBC_MBC3 * 2: hipLaunchKernelGGL((step_kernel<MBC_MBC3, false>), g, b, 0, st, s, a); break;

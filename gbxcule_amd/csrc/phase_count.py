@@ -4,7 +4,7 @@ Copies the kernel sources to a temporary directory, inserts assembler
 comments at the phase boundaries of the loop (fetch, bus reads, datapath,
 next-record load, write phase, fast tail, loop back edge) and at the head of
 each block the loop hints as rare, compiles the device code for gfx950 to
-assembly and walks ``step_kernel<ROM_ONLY, no debug>`` along the compiler's
+assembly and walks ``step_kernel<ROM_ONLY, no debug, no cart RAM>`` along the compiler's
 fall-through layout: an unconditional branch is followed, a conditional
 branch falls through, except an ``s_cbranch_execz`` whose skipped region
 opens with a rare-block marker, which is taken (no lane runs the rare block).
@@ -27,7 +27,7 @@ CSRC = Path(__file__).resolve().parent
 INCLUDE = CSRC.parent.parent / "include"
 sys.path.insert(0, str(CSRC.parent))
 from build import DEVICE_FLAGS  # noqa: E402  (the flags the library is built with)
-KERNEL = "_ZN3gbx12_GLOBAL__N_111step_kernelILi0ELb0E"  # step_kernel<MBC_ROM_ONLY, false>
+KERNEL = "_ZN3gbx12_GLOBAL__N_111step_kernelILi0ELb0ELb0E"  # step_kernel<MBC_ROM_ONLY, false, false>
 PHASES = ("fetch", "bus", "exec", "nextrec", "write", "tail", "loop")
 LABELS = {
     "fetch": "fetch (record valid check)",
@@ -172,7 +172,7 @@ def main() -> int:
     size = lambda b: sum(1 for x in b if (s := x.strip()) and s[0] not in ";.#" and not re.match(r"^[.\w$]+:", s))  # noqa: E731
     res = walk(*parse(mk))
     cols = ("VALU", "SALU", "branch", "VMEM", "wait/nop")
-    L = ["# Step kernel hot loop, static instructions per phase (gfx950, step_kernel<ROM_ONLY, no debug>)",
+    L = ["# Step kernel hot loop, static instructions per phase (gfx950, step_kernel<ROM_ONLY, no debug, no cart RAM>)",
          f"Command: python gbxcule_amd/csrc/phase_count.py  (kernel size {size(pl)} instructions as built, "
          f"{size(mk)} with the phase markers)", "",
          "| Phase | " + " | ".join(cols) + " | all |", "|---" * (len(cols) + 2) + "|"]
