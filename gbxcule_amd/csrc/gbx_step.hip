@@ -18,16 +18,25 @@
 //    record, with one shared adder, logic unit, shifter and 16-bit adder, so
 //    no lane waits for another lane's opcode class;
 //  * bus reads compute one address per lane (ROM window, boot image,
-//    cartridge RAM or the env's memory) and issue at most two loads; only IO
-//    side effects, MBC and cartridge-RAM writes take divergent branches;
+//    cartridge RAM or the env's memory) and every lane loads its byte, with
+//    no branch around the load; only a second byte, IO side effects, MBC and
+//    cartridge-RAM writes take divergent branches;
 //  * CPU registers, the hot IO registers and the cartridge bank offsets live
 //    in VGPRs for the whole launch and are written back once;
+//  * a step that reaches no event (timer, scanline, frame end, pending
+//    request) takes a fast tail that only advances DIV, the scanline
+//    position and the cycle counters; scanline changes that raise no
+//    request and TIMA edges short of an overflow are run through without
+//    being applied, and are settled before anything observes them (LY,
+//    STAT, TIMA and DIV reads derive their values instead);
 //  * a halted CPU, an LY poll loop and a block-copy loop advance in one step
 //    to the first event the reference's per-instruction loop could observe
 //    (ff_horizon), which is exactly equivalent to stepping them one
 //    instruction (or 4 halted cycles) at a time;
-//  * the rare paths carry branch-probability hints so that the common path
-//    is laid out as straight fall-through code.
+//  * the rare paths carry branch-probability hints, and those of the
+//    per-instruction path a wave-uniform ballot test, so that the common
+//    path is laid out as straight fall-through code that keeps its exec
+//    mask.
 #include "gbx_internal.h"
 // after gbx_internal.h, which brings in the HIP runtime
 #include "gbx_exec.h"
