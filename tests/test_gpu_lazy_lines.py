@@ -10,8 +10,8 @@ loops of seeded, joypad-dependent lengths and read LY, STAT, TIMA and DIV
 through LDH, LD A,(C) and LD A,(HL) at whatever position the loop ends,
 folding each byte into work RAM.  Interrupt handlers read LY and STAT too
 and move LYC; the window is on in some carts (its line counter is part of
-the compared state), some carts write LY, DIV, TIMA and TAC, the timer runs
-at every rate, and env 0 (which applies every scanline change) shares a
+the compared state), some carts write LY, DIV, TIMA and TAC or switch the
+LCD off and on, the timer runs at every rate, and env 0 (which applies every scanline change) shares a
 wavefront with envs that defer.  State is compared in full after every step.
 """
 
@@ -31,7 +31,7 @@ pytestmark = pytest.mark.gpu
 
 
 def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, ly_write: bool,
-              timer_writes: bool = False) -> bytes:
+              timer_writes: bool = False, lcd_toggle: bool = False) -> bytes:
     rng = np.random.default_rng(seed)
     rom = bytearray(0x8000)
     h = Asm(origin=0x0068)
@@ -119,6 +119,13 @@ def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, 
             a.ldh_a8_a(0x44)  # the next change overwrites it
             a.ldh_a_a8(0x44)
             a.ld_a16_a(0xC010)
+        if lcd_toggle and i == 8:  # LCD off and on again after a delay-loop's deferred lines
+            a.ld_r_d8("A", 0x11)
+            a.ldh_a8_a(0x40)
+            a.ldh_a_a8(0x44)
+            a.ld_a16_a(0xC01E)
+            a.ld_r_d8("A", 0xB1 if window else 0x91)
+            a.ldh_a8_a(0x40)
         if timer_writes and i in (3, 7, 10):
             if i == 3:
                 a.ldh_a8_a(0x04)  # DIV reset
@@ -139,7 +146,7 @@ def lazy_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, window: bool, 
 
 CASES = [
     # seed, IME, IE, TAC, STAT sources (HBlank 0x08, VBlank 0x10, OAM 0x20, LYC 0x40), window, LY write,
-    # DIV/TIMA/TAC writes
+    # DIV/TIMA/TAC writes[, LCD switched off and on]
     (1, True, 0x03, 0x00, 0x40, True, False, False),
     (2, True, 0x01, 0x05, 0x10, False, False, False),
     (3, False, 0x00, 0x00, 0x00, True, False, False),
@@ -151,15 +158,18 @@ CASES = [
     (9, False, 0x04, 0x06, 0x40, True, False, True),
     (10, True, 0x05, 0x07, 0x10, False, True, True),
     (11, True, 0x07, 0x04, 0x08, True, False, True),
+    (12, True, 0x03, 0x05, 0x40, True, False, False, True),
+    (13, False, 0x01, 0x00, 0x10, False, True, True, True),
 ]
 
 
-@pytest.mark.parametrize("seed,ime,ie,tac,stat,window,ly_write,timer_writes", CASES)
-def test_lazy_scanline_parity(bootstub, seed, ime, ie, tac, stat, window, ly_write, timer_writes):
+@pytest.mark.parametrize("case", CASES, ids=[str(c[0]) for c in CASES])
+def test_lazy_scanline_parity(bootstub, case):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
 
-    rom = lazy_cart(seed, ime, ie, tac, stat, window, ly_write, timer_writes)
+    seed, ime, ie, tac, stat = case[:5]
+    rom = lazy_cart(*case)
     n, fs, steps = 128, 6, 4
     dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=3,
                         stage="emulate_only", bootrom=bootstub)  # fmt: skip
@@ -177,9 +187,11 @@ def test_lazy_scanline_parity(bootstub, seed, ime, ie, tac, stat, window, ly_wri
         mem = ref.mem
         # the reads saw different positions in different envs
         assert len({bytes(mem[e, 0xC000:0xC00C]) for e in range(n)}) > 1
-        if ime and ie & 1:
+        lcd_toggle = len(case) > 8 and case[8]
+        # (switching the LCD off each pass never reaches line 144 or, here, LYC)
+        if ime and ie & 1 and not lcd_toggle:
             assert int(mem[1, 0xDF00]) > 0  # VBlank interrupts were serviced
-        if ime and ie & 2 and stat & 0x48:
+        if ime and ie & 2 and stat & 0x48 and not lcd_toggle:
             assert int(mem[1, 0xDF01]) > 0  # STAT interrupts were serviced
         if ime and ie & 4 and tac & 4:
             assert int(mem[1, 0xDF02]) > 0  # timer interrupts were serviced
