@@ -181,8 +181,9 @@ struct Lane {
   uint32_t rtc_halt, rtc_dirty;
   uint32_t map_changed;  // set when a write remaps the fetch windows
   // Cycles a step may take on the fast path (event_budget).  Every event the
-  // fast path must not pass sets it to 0: writes with side effects, MBC and
-  // RTC writes, traps; the slow path recomputes it.
+  // fast path must not pass sets it to 0: IO and RTC writes with side
+  // effects, traps, EI, RETI and HALT with a request pending; the slow path
+  // recomputes it.
   int budget;
   // frame loop
   int frames_done, release;
@@ -580,8 +581,7 @@ struct Lane {
       return;
     }
     refresh_cart();
-    map_changed = 1;
-    budget = 0;
+    map_changed = 1;  // write_bus drops the prefetched record
   }
   __device__ void write_special(uint32_t x, uint32_t v) {
     if (x < 0x8000u) {
@@ -628,13 +628,19 @@ struct Lane {
   __device__ static bool plain_store(uint32_t x) { return plain_ram(x) | (x == 0xFF00u); }
   // The instruction's bus writes, in order (n = 0, 1 or 2).  When both are
   // plain stores they are stored without a branch; a lane with one write
-  // stores its first byte twice.
-  __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1) {
+  // stores its first byte twice.  An MBC bank write clears rv, the validity
+  // of the record already fetched for the next pc (the boot ROM switch is an
+  // IO write, after which the full sequence drops the record).
+  __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1, bool& rv) {
     const uint32_t x0 = a0 & 0xFFFFu, x1 = a1 & 0xFFFFu;
     const bool two = n >= 2u;
     if (__builtin_expect((!plain_store(x0)) | (two & !plain_ram(x1)), 0)) {
       write8(a0, v0);
       if (two) write8(a1, v1);
+      if (mbc != MBC_ROM_ONLY) {
+        rv = rv & (map_changed == 0u);
+        map_changed = 0;
+      }
     } else {
       const bool j0 = x0 == 0xFF00u;
       const uint32_t s0 = j0 ? joyp_read(v0) : v0;
@@ -1007,9 +1013,13 @@ struct Lane {
                        : ((scan | ly | wl | lym) != 0u ? 0 : b);
     if ((mbc == MBC_MBC3) & (rtc_halt == 0u))  // the next RTC second
       b = ((rtc_dirty != 0u) | (rtc_sub < 0)) ? 0 : min(b, kRtcCyclesPerSecond - rtc_sub);
-    // a pending TIMA reload, EI delay, interrupt request or bank remap takes
-    // the full sequence every step until it is dealt with
-    return (pend | ime_delay | (ie & ifr & 0x1Fu) | map_changed) != 0u ? 0 : b;
+    // a pending TIMA reload or EI delay, or an interrupt request that IME
+    // or HALT lets act on, takes the full sequence every step until it is
+    // dealt with.  With IME clear a running CPU leaves a request pending and
+    // the step's interrupt check does nothing; EI, RETI and HALT, which
+    // change that, zero the budget when a request is pending.
+    const uint32_t irq = ((ime | halted) != 0u) ? (ie & ifr & 0x1Fu) : 0u;
+    return (pend | ime_delay | irq) != 0u ? 0 : b;
   }
   // Cycles a halted CPU advances in one loop iteration: the reference steps
   // 4 cycles at a time and wakes on IE & IF; nothing it can observe changes
@@ -1299,6 +1309,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
             L.ime_delay = 0;
           }
           if (o.misc & 4u) L.halted = 1;
+          // the step's interrupt check services or wakes on a pending request
+          if (((L.ime | L.halted) != 0u) & ((L.ie & L.ifr & 0x1Fu) != 0u)) L.budget = 0;
           if (o.misc & 8u) {  // misc.py:42-56: freeze the env, pc unchanged
             trap = 1;
             trap_pc = (int)pc;
@@ -1364,7 +1376,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
 
     // ---- write phase, debug checks, timer, PPU, interrupt check --------------
     int svc = 0;
-    if (__builtin_expect(wn != 0u, 1)) L.write_bus(wn, wa0, wv0, wa1, wv1);
+    if (__builtin_expect(wn != 0u, 1)) L.write_bus(wn, wa0, wv0, wa1, wv1, rv);
     if (dbg) {
       if (!hiter) {
         if (dbg_rst38 && L.pc >= 0xFE00u && !trap) {

@@ -6,9 +6,13 @@ anywhere, so reads and writes also hit IO, MBC and cart-RAM side effects.
 
 After 1, 2 and 6 instructions (debug max-instruction trap) and after one full
 frame of continued execution of the random ROM, the whole state must match.
+GBX_ISA_SEEDS=k adds k more random states per cart, each compared after every
+one of 8 frames (about 2 s per seed and cart).
 """
 
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -23,6 +27,7 @@ pytestmark = pytest.mark.gpu
 
 OPS = [op for op in range(256) if op != 0xCB] + [0x100 | cb for cb in range(256)]
 CARTS = [(0x00, 0x00, 0x00), (0x01, 0x02, 0x00), (0x13, 0x02, 0x03)]
+SEEDS = [0] + list(range(1, 1 + int(os.environ.get("GBX_ISA_SEEDS", "0"))))
 
 
 def _rom(rng, cart_type, rom_code, ram_code, pcs, ops):
@@ -89,13 +94,15 @@ def _clear_traps(ref, dut):
         dut.import_field(f, np.zeros(dut.num_envs, np.int64))
 
 
+@pytest.mark.parametrize("seed", SEEDS)
 @pytest.mark.parametrize("cart", CARTS, ids=["rom_only", "mbc1", "mbc3_ram"])
-def test_every_opcode_from_random_states(bootstub, cart):
+def test_every_opcode_from_random_states(bootstub, cart, seed):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
     from oracle.ref import RefMachine
 
-    rng = np.random.default_rng(1234 + cart[0])
+    rng = np.random.default_rng(1234 + cart[0] if seed == 0 else seed * 7919 + cart[0])
+    frames = 1 if seed == 0 else 8
     reps = 2
     ops = np.array(OPS * reps)
     n = ops.size
@@ -117,9 +124,10 @@ def test_every_opcode_from_random_states(bootstub, cart):
             _clear_traps(ref, dut)
         ref.set_debug()
         dut.set_debug_traps()
-        ref.step(acts, 1, 8, "full_step", threads=8)
-        dut.step(acts)
-        assert_same_state(dut, ref, step=99, tag=f"{cart} frame")
+        for f in range(frames):
+            ref.step(acts, 1, 8, "full_step", threads=8)
+            dut.step(acts)
+            assert_same_state(dut, ref, step=99 + f, tag=f"{cart} seed {seed} frame {f}")
         np.testing.assert_array_equal(dut.export_latches(), ref.latches)
     finally:
         dut.close()
