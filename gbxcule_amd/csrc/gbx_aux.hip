@@ -1,6 +1,7 @@
 // gbx_aux.hip -- kernels around the step: power-on fill, the 2x-downsampled
 // snapshot renderer, reset snapshot / masked restore, RAM-sense gather, state
 // hash, and the layout converters behind the export/import helpers.
+#include <type_traits>
 #include <utility>
 
 #include "gbx_aux.h"
@@ -38,15 +39,10 @@ __global__ void init_state_kernel(int32_t* cs, int32_t* sc, int npad, int mbc_ki
 }
 
 // ---------------------------------------------------------------------------
-// Snapshot renderer (reference kernels/ppu_render_downsampled.py:27-234).
-// One thread per (env, output row); lanes of a wavefront are consecutive envs
-// of one row, so IO/OAM reads of the same address coalesce.  Per row, the
-// sprites (the first 10 OAM entries overlapping the line, counted before the
-// x test) are resolved once into a line buffer of the 80 samples: each
-// sample keeps the opaque sprite pixel with the lowest x (ties: the lower
-// OAM index, the earlier entry), as the reference's per-sample search over
-// OAM selects it.  The BG/window tile row is re-read only when the sample
-// moves to another tile.
+// Snapshot renderer (reference kernels/ppu_render_downsampled.py:27-234),
+// render_kernel below, and env 0's full frame (frame_bg_kernel).  Row reads
+// one env's bytes straight from the env-interleaved memory (the full-frame
+// renderer's source); the snapshot renderer reads an LDS image (Img).
 // ---------------------------------------------------------------------------
 struct Row {
   const uint8_t* mb;  // block base
@@ -64,10 +60,31 @@ __device__ uint32_t bg_tile_addr(uint32_t lcdc, uint32_t tile_id) {
   return (uint32_t)(0x9000 + ((int)tile_id >= 128 ? (int)tile_id - 256 : (int)tile_id) * 16);
 }
 
-constexpr int kRenderRows = 4;  // output rows per workgroup, one wavefront each
-constexpr int kRenderThreads = kEnvBlock * kRenderRows;
-constexpr int kTileSlots = 21;          // tile columns one 80-sample row can touch
-constexpr int kGroups = kDsW / 4;       // 4-sample groups per row (one output word unpacked)
+// The snapshot render reads each env's video RAM, OAM and LCD registers from
+// an LDS image of 8 envs (one eighth of a 64-env memory block): address row
+// a of the image holds the 8 envs' bytes of address a, as they sit side by
+// side in the env-interleaved layout, so one 8-byte load fills a row.
+// Gathered straight from memory, every byte a lane needs lies on a 64-byte
+// line of its own (the other lanes read other addresses), and the render
+// was bound by the cache's line lookups.
+constexpr int kImgEnvs = 8;
+constexpr uint32_t kImgVram = 0x2000u;  // 8000-9FFF
+constexpr uint32_t kImgOam = 0xA0u;     // FE00-FE9F
+constexpr uint32_t kImgRegs = 0x0Cu;    // FF40-FF4B
+constexpr uint32_t kImgRows = kImgVram + kImgOam + kImgRegs;
+constexpr int kImgThreads = kImgEnvs * kDsH;  // one per (env, output row)
+constexpr int kImgLoads = (int)((kImgRows + kImgThreads - 1) / kImgThreads);
+constexpr int kTileSlots = 21;     // tile columns one 80-sample row can touch
+constexpr int kGroups = kDsW / 4;  // 4-sample groups per row (one output word unpacked)
+static_assert(kImgEnvs == 8, "image rows are 8 bytes");
+
+struct Img {
+  const uint8_t* p;  // the workgroup's image
+  uint32_t env;      // 0..7
+  __device__ uint32_t M(uint32_t addr) const { return p[((addr - 0x8000u) << 3) | env]; }  // video RAM
+  __device__ uint32_t oam(uint32_t i) const { return p[((kImgVram + i) << 3) | env]; }
+  __device__ uint32_t reg(uint32_t addr) const { return p[((kImgVram + kImgOam + addr - 0xFF40u) << 3) | env]; }
+};
 
 // The four sampled pixels of one tile row word t = lo | hi << 8, colours
 // (0..3) one per byte, byte i = the i-th sampled pixel from the left: bits
@@ -88,15 +105,16 @@ __device__ __forceinline__ uint32_t spread_tile(uint32_t t, uint32_t p) {
 // c[j] = the sampled colours (spread_tile) of map column ((s >> 3) + j) & 31.
 // Sample ox is then byte ox + ((s & 7) >> 1) of the byte stream c[0], c[1], ...
 // The 21 map reads of a layer are independent (layer_ids), then its 42
-// tile-data reads are (layer_tiles); the caller issues both layers' map
-// reads before either layer's tile reads.
-__device__ __forceinline__ void layer_ids(const Row& r, uint32_t map, uint32_t s, uint32_t py,
+// tile-data reads are (layer_tiles).
+template <class Src>
+__device__ __forceinline__ void layer_ids(const Src& r, uint32_t map, uint32_t s, uint32_t py,
                                           uint32_t (&id)[kTileSlots]) {
   const uint32_t mrow = map + (py >> 3) * 32u;
 #pragma unroll
   for (int j = 0; j < kTileSlots; ++j) id[j] = r.M(mrow + (((s >> 3) + (uint32_t)j) & 31u));
 }
-__device__ __forceinline__ void layer_tiles(const Row& r, uint32_t lcdc, uint32_t s, uint32_t py,
+template <class Src>
+__device__ __forceinline__ void layer_tiles(const Src& r, uint32_t lcdc, uint32_t s, uint32_t py,
                                             const uint32_t (&id)[kTileSlots], uint32_t (&c)[kTileSlots]) {
   const uint32_t row2 = (py & 7u) * 2u;
 #pragma unroll
@@ -106,217 +124,298 @@ __device__ __forceinline__ void layer_tiles(const Row& r, uint32_t lcdc, uint32_
   }
 }
 
-// Store one output row of the block's 64 envs from the staging area: lanes
-// run along each env's row (W words), so one store instruction covers about
-// 64*4/(4*W) envs' rows instead of 64 rows 5,760 bytes apart.
-template <int W>
-__device__ __forceinline__ void store_rows(const uint32_t* stage, uint8_t* rows, size_t env_bytes, uint32_t blk,
-                                           uint32_t lane, uint32_t n, bool aligned) {
-#pragma unroll
-  for (int i = 0; i < W; ++i) {
-    const uint32_t d = (uint32_t)i * kEnvBlock + lane;
-    const uint32_t env = d / W, w = d % W;
-    const uint32_t v = stage[w * kEnvBlock + (env ^ w)];
-    if (blk * kEnvBlock + env < n) {
-      uint8_t* p = rows + env * env_bytes + 4u * w;
-      if (aligned) {
-        *reinterpret_cast<uint32_t*>(p) = v;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = (uint8_t)(v >> (8 * q));
-      }
+// One workgroup per 8 envs: it copies their image rows into LDS (every
+// thread issues all its loads before its LDS stores), then renders one
+// (env, output row) per thread.  The 8 workgroups of a 64-env block are
+// dealt to one XCD (the hardware deals workgroup i to XCD i mod 8), so each
+// 64-byte line comes from HBM about once and its other reads hit that XCD's
+// L2.  Per row, the sprites (the first 10 OAM entries covering the line,
+// counted before the x test) are resolved into a line buffer of the 80
+// samples: each sample keeps the opaque sprite pixel with the lowest x
+// (ties: the lower OAM index, the earlier entry), as the reference's
+// per-sample search over OAM selects it; a thread walks only its covering
+// entries, two per round.  The BG and window tile rows are read for all 21
+// tile columns at once; the samples are then shaded four at a time, one per
+// byte: the group's colours are a byte window of the layer's colour stream,
+// the window layer is blended in by a byte mask, BGP maps colours to shades
+// through a byte permute, and the sprite overlay is a byte mask.  The output
+// words are staged in LDS in output order and stored by each wavefront
+// along the rows of its 8 envs.
+template <bool packed>
+__global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
+                                                             uint32_t rounds) {
+  __shared__ __align__(16) uint8_t img[kImgRows * kImgEnvs];
+  // OAM entries covering each (env, output row): bit k = entry k
+  __shared__ uint64_t cover[kDsH][kImgEnvs];
+  // sprite line buffer, 4 samples per (group, thread): 0 = no sprite pixel,
+  // else bits [0:1] its shade (palette applied), [2] behind non-zero BG, [3]
+  // set, [8:15] the sprite's OAM x (its left edge + 8); reused as the
+  // output stage
+  __shared__ __align__(16) uint16_t obj[kGroups][kImgThreads][4];
+  const uint32_t tid0 = threadIdx.x;
+  const uint32_t nblk = (uint32_t)s.npad >> kEnvBlockShift;
+  // Group `it` of this workgroup: (64-env block, eighth).  With rounds > 1
+  // the grid is a multiple of 64 workgroups, each rendering `rounds` groups;
+  // in round `it` the workgroups of one XCD render whole blocks.
+  auto group = [&](uint32_t it, uint32_t& blk, uint32_t& part) {
+    const uint32_t w = blockIdx.x;
+    if (rounds > 1u) {
+      const uint32_t c = w >> 3, per_xcd = gridDim.x >> 3;
+      blk = ((it * (per_xcd >> 3) + (c >> 3)) << 3) | (w & 7u);
+      part = c & 7u;
+    } else if ((nblk & 7u) == 0u) {
+      blk = (((w >> 3) >> 3) << 3) | (w & 7u);
+      part = (w >> 3) & 7u;
+    } else {
+      blk = w >> 3;
+      part = w & 7u;
     }
-  }
-}
-
-// One workgroup per 64-env memory block and 4 output rows; lanes are the
-// block's envs, so every read of one address by a wavefront is one 64-byte
-// row.  The block's OAM is staged into LDS once for the 4 rows, and with it,
-// per entry and row, whether the entry covers the row (position valid, row
-// inside its 8 or 16 lines).  Per row, the sprites (the first 10 OAM
-// entries covering the line, counted before the x test) are resolved into a
-// line buffer of the 80 samples: each sample keeps the opaque sprite pixel
-// with the lowest x (ties: the lower OAM index, the earlier entry), as the
-// reference's per-sample search over OAM selects it.  A lane walks only its
-// own covering entries, in OAM order, two per round.  The BG and window tile
-// rows are fetched for all 21 tile columns at once; the samples are then
-// shaded four at a time, one per byte: the group's colours are a byte window
-// of the layer's colour stream, the window layer is blended in by a byte
-// mask, BGP maps colours to shades through a byte permute, and the sprite
-// overlay is a byte mask.
-__global__ __launch_bounds__(kRenderThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
-                                                                int packed) {
-  // OAM entry k of each env: y | x << 8 | tile << 16 | attr << 24
-  __shared__ uint32_t oam[40][kEnvBlock];
-  // entries 10w .. 10w + 9 (staged by wavefront w) covering row r: bit i
-  __shared__ uint16_t cover[kRenderRows][kRenderRows][kEnvBlock];
-  // sprite line buffer per row, 4 samples per (group, lane): 0 = no sprite
-  // pixel, else bits [0:1] its shade (palette applied), [2] behind non-zero
-  // BG, [3] set, [8:15] the sprite's OAM x (its left edge + 8)
-  __shared__ __align__(16) uint16_t obj[kRenderRows][kGroups][kEnvBlock][4];
-  static_assert(kRenderRows * 10 == 40, "each wavefront stages 10 OAM entries");
-  const uint32_t lane = threadIdx.x & (kEnvBlock - 1);
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> kEnvBlockShift);
-  const uint32_t blk = blockIdx.x;
-  const Row r{s.mem + ((size_t)blk << 22), lane};  // the block's spare lanes render but never store
-  const uint32_t lcdc = r.M(0xFF40);
-  const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
-  const uint32_t y0 = blockIdx.y * kRenderRows * 2u;  // screen row of the workgroup's first output row
-  {
-    uint32_t cv[kRenderRows] = {};
+  };
+  // image rows k0 <= k < k1 of each thread for a group, the loads issued
+  // together
+  uint2 v[kImgLoads];
+  auto fetch = [&](uint32_t blk, uint32_t part, auto k0, auto k1) {
+    const uint8_t* src = s.mem + ((size_t)blk << 22) + part * (uint32_t)kImgEnvs;
+    // (recomputed per call: kept across the loop, the 15 offsets would hold
+    // registers the render needs)
+    uint32_t t = tid0;
+    asm volatile("" : "+v"(t));
 #pragma unroll
-    for (uint32_t i = 0; i < 10u; ++i) {
-      const uint32_t k = 10u * wv + i;
-      const uint32_t a = 0xFE00u + 4u * k;
-      const uint32_t sy = r.M(a), sx = r.M(a + 1u);
-      oam[k][lane] = sy | (sx << 8) | (r.M(a + 2u) << 16) | (r.M(a + 3u) << 24);
-      const bool valid = (sx != 0u) & (sy != 0u) & (sx < 168u) & (sy < 160u);
-#pragma unroll
-      for (int q = 0; q < kRenderRows; ++q)  // row y0 + 2q inside [sy - 16, sy - 16 + height)
-        cv[q] |= (uint32_t)(valid & (y0 + 2u * (uint32_t)q + 16u - sy < height)) << i;
+    for (int k = decltype(k0)::value; k < decltype(k1)::value; ++k) {
+      const uint32_t i = min(t + (uint32_t)k * kImgThreads, kImgRows - 1u);
+      const uint32_t a = i < kImgVram ? 0x8000u + i
+                         : i < kImgVram + kImgOam ? 0xFE00u + (i - kImgVram)
+                                                  : 0xFF40u + (i - kImgVram - kImgOam);
+      v[k] = *reinterpret_cast<const uint2*>(src + ((size_t)a << kEnvBlockShift));
     }
-#pragma unroll
-    for (int q = 0; q < kRenderRows; ++q) cover[q][wv][lane] = (uint16_t)cv[q];
-  }
-  const uint32_t oy = blockIdx.y * kRenderRows + wv;
-  const uint32_t y = oy * 2u;
-  const uint32_t scy = r.M(0xFF42), scx = r.M(0xFF43);
-  const uint32_t bgp = r.M(0xFF47), obp0 = r.M(0xFF48), obp1 = r.M(0xFF49);
-  const uint32_t wy = r.M(0xFF4A), wx = r.M(0xFF4B);
-  uint16_t (&line)[kGroups][kEnvBlock][4] = obj[wv];
-#pragma unroll
-  for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&line[g][lane][0]) = make_uint2(0u, 0u);
-  __syncthreads();
-  if (lcdc & 0x02u) {
-    // the entries covering this row in OAM order, then only the first 10
-    uint64_t vis = 0;
-#pragma unroll
-    for (int w = 0; w < kRenderRows; ++w) vis |= (uint64_t)cover[wv][w][lane] << (10 * w);
-    if (__builtin_expect(__ballot(__popcll(vis) > 10) != 0u, 0)) {
-      uint64_t rest = vis;
-#pragma unroll
-      for (int j = 0; j < 10; ++j) rest &= rest - 1u;  // clears the lowest 10
-      vis &= ~rest;
-    }
-    // each lane's covering entries, lowest OAM index first, two per round
-    // (their tile-row loads issued together)
+  };
+  uint32_t blk, part;
+  using K0 = std::integral_constant<int, 0>;
+  using KH = std::integral_constant<int, kImgLoads / 2 + 1>;
+  using KN = std::integral_constant<int, kImgLoads>;
+  group(0u, blk, part);
+  fetch(blk, part, K0{}, KN{});
 #pragma unroll 1
-    while (__ballot(vis != 0u) != 0u) {
-      uint32_t ent[2], lo[2], hi[2];
-      bool on[2];
+  for (uint32_t it = 0; it < rounds; ++it) {
+    // (derived per round: kept across the loop, the addresses that follow
+    // from the thread index would hold registers the render needs)
+    uint32_t tid = tid0;
+    asm volatile("" : "+v"(tid));
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        on[t] = vis != 0u;
-        const uint32_t k = on[t] ? (uint32_t)__builtin_ctzll(vis) : 0u;
-        vis &= vis - 1u;
-        ent[t] = oam[k][lane];
+    for (int k = 0; k < kImgLoads; ++k) {
+      const uint32_t i = tid + (uint32_t)k * kImgThreads;
+      if (i < kImgRows) *reinterpret_cast<uint2*>(img + (size_t)i * kImgEnvs) = v[k];
+    }
+    // the next group's rows load while this one renders: the first half
+    // now, the rest once the tile rows below no longer hold registers
+    uint32_t nblk_next = 0, npart = 0;
+    const bool more = it + 1u < rounds;
+    if (more) {
+      group(it + 1u, nblk_next, npart);
+      fetch(nblk_next, npart, K0{}, KH{});
+    }
+    const uint32_t env = tid & (uint32_t)(kImgEnvs - 1);
+    const uint32_t oy = tid / (uint32_t)kImgEnvs;
+    const uint32_t y = oy * 2u;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&obj[g][tid][0]) = make_uint2(0u, 0u);
+    cover[oy][env] = 0u;
+    __syncthreads();
+    const Img r{img, env};
+    // entry k of env e (thread 40e + k) marks the output rows it covers:
+    // position valid, screen row 2*oy inside [sy - 16, sy - 16 + height)
+    if (tid < 40u * (uint32_t)kImgEnvs) {
+      const uint32_t e = tid / 40u, k = tid % 40u;
+      const Img o{img, e};
+      const uint32_t sy = o.oam(4u * k), sx = o.oam(4u * k + 1u);
+      const uint32_t ht = (o.reg(0xFF40) & 0x04u) ? 16u : 8u;
+      if ((sx != 0u) & (sy != 0u) & (sx < 168u) & (sy < 160u)) {
+        const uint32_t first = (sy > 16u ? sy - 16u : 0u) >> 1;
+#pragma unroll
+        for (uint32_t j = 0; j < 9u; ++j) {
+          const uint32_t row = first + j;
+          if ((row < (uint32_t)kDsH) & (2u * row + 16u - sy < ht))
+            atomicOr(reinterpret_cast<unsigned long long*>(&cover[row][e]), 1ull << k);
+        }
       }
+    }
+    __syncthreads();
+    const uint32_t lcdc = r.reg(0xFF40);
+    const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
+    const uint32_t scy = r.reg(0xFF42), scx = r.reg(0xFF43);
+    const uint32_t bgp = r.reg(0xFF47), obp0 = r.reg(0xFF48), obp1 = r.reg(0xFF49);
+    const uint32_t wy = r.reg(0xFF4A), wx = r.reg(0xFF4B);
+    if (lcdc & 0x02u) {
+      // the entries covering this row (position valid, row inside their 8 or
+      // 16 lines) in OAM order, then only the first 10
+      uint64_t vis = cover[oy][env];
+      if (__builtin_expect(__ballot(__popcll(vis) > 10) != 0u, 0)) {
+        uint64_t rest = vis;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint32_t sy = ent[t] & 0xFFu;
-        const int top = (int)sy - 16;
-        uint32_t tile = (ent[t] >> 16) & 0xFFu;
-        const uint32_t attr = ent[t] >> 24;
-        uint32_t row = (uint32_t)((int)y - top) & 15u;
-        if ((attr >> 6) & 1u) row = (height - 1u - row) & 15u;
-        if (height == 16u) {
-          tile &= 0xFEu;
-          if (row >= 8u) {
-            tile += 1u;
-            row -= 8u;
+        for (int j = 0; j < 10; ++j) rest &= rest - 1u;  // clears the lowest 10
+        vis &= ~rest;
+      }
+      // each thread's covering entries, lowest OAM index first, two per round
+      // (their tile-row reads issued together)
+#pragma unroll 1
+      while (__ballot(vis != 0u) != 0u) {
+        uint32_t ent[2], lo[2], hi[2];
+        bool on[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          on[t] = vis != 0u;
+          const uint32_t k = on[t] ? (uint32_t)__builtin_ctzll(vis) : 0u;
+          vis &= vis - 1u;
+          ent[t] = r.oam(4u * k) | (r.oam(4u * k + 1u) << 8) | (r.oam(4u * k + 2u) << 16) |
+                   (r.oam(4u * k + 3u) << 24);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint32_t sy = ent[t] & 0xFFu;
+          const int top = (int)sy - 16;
+          uint32_t tile = (ent[t] >> 16) & 0xFFu;
+          const uint32_t attr = ent[t] >> 24;
+          uint32_t row = (uint32_t)((int)y - top) & 15u;
+          if ((attr >> 6) & 1u) row = (height - 1u - row) & 15u;
+          if (height == 16u) {
+            tile &= 0xFEu;
+            if (row >= 8u) {
+              tile += 1u;
+              row -= 8u;
+            }
+          }
+          const uint32_t ta = 0x8000u + tile * 16u + (row & 7u) * 2u;
+          lo[t] = on[t] ? r.M(ta) : 0u;
+          hi[t] = on[t] ? r.M(ta + 1u) : 0u;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          if (!on[t]) continue;
+          const uint32_t sx = (ent[t] >> 8) & 0xFFu;
+          const uint32_t attr = ent[t] >> 24;
+          const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
+          const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
+          const int left = (int)sx - 8;
+          // the sampled columns x = 2*ox inside [left, left + 8)
+          for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
+            if (x < 0 || x >= 2 * kDsW) continue;
+            const uint32_t pxl = (uint32_t)(x - left);
+            const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
+            const uint32_t color = (((hi[t] >> bit) & 1u) << 1) | ((lo[t] >> bit) & 1u);
+            if (color == 0) continue;
+            const uint32_t ox = (uint32_t)x >> 1;
+            uint16_t& slot = obj[ox >> 2][tid][ox & 3u];
+            const uint32_t cur = slot;
+            if (cur == 0 || sx < (cur >> 8)) slot = (uint16_t)(tag | ((pal >> (color * 2u)) & 3u));
           }
         }
-        const uint32_t ta = 0x8000u + tile * 16u + (row & 7u) * 2u;
-        lo[t] = on[t] ? r.M(ta) : 0u;
-        hi[t] = on[t] ? r.M(ta + 1u) : 0u;
-      }
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (!on[t]) continue;
-        const uint32_t sx = (ent[t] >> 8) & 0xFFu;
-        const uint32_t attr = ent[t] >> 24;
-        const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
-        const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
-        const int left = (int)sx - 8;
-        // the sampled columns x = 2*ox inside [left, left + 8)
-        for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
-          if (x < 0 || x >= 2 * kDsW) continue;
-          const uint32_t pxl = (uint32_t)(x - left);
-          const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
-          const uint32_t color = (((hi[t] >> bit) & 1u) << 1) | ((lo[t] >> bit) & 1u);
-          if (color == 0) continue;
-          const uint32_t ox = (uint32_t)x >> 1;
-          uint16_t& slot = line[ox >> 2][lane][ox & 3u];
-          const uint32_t cur = slot;
-          if (cur == 0 || sx < (cur >> 8)) slot = (uint16_t)(tag | ((pal >> (color * 2u)) & 3u));
-        }
       }
     }
-  }
 
-  const uint32_t bg_on = (lcdc & 0x01u) ? ~0u : 0u;
-  const bool win = (lcdc & 0x20u) && y >= wy;
-  const int wx7 = (int)wx - 7;
-  const uint32_t sw = (7u - wx) & 0xFFu;  // window: px = (x - (WX - 7)) & 0xFF
-  uint32_t cb[kTileSlots], cw[kTileSlots];
+    const uint32_t bg_on = (lcdc & 0x01u) ? ~0u : 0u;
+    const bool win = (lcdc & 0x20u) && y >= wy;
+    const int wx7 = (int)wx - 7;
+    const uint32_t sw = (7u - wx) & 0xFFu;  // window: px = (x - (WX - 7)) & 0xFF
+    uint32_t cb[kTileSlots], cw[kTileSlots];
 #pragma unroll
-  for (int j = 0; j < kTileSlots; ++j) cb[j] = cw[j] = 0;
-  if (bg_on) {
-    // the background unless the window covers the whole row
-    const bool do_bg = !(win && wx7 <= 0), do_win = win && wx7 < 2 * kDsW - 1;
-    const uint32_t pyb = (y + scy) & 0xFFu, pyw = (y - wy) & 0xFFu;
-    uint32_t idb[kTileSlots], idw[kTileSlots];
-    if (do_bg) layer_ids(r, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, pyb, idb);
-    if (do_win) layer_ids(r, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, pyw, idw);
-    if (do_bg) layer_tiles(r, lcdc, scx, pyb, idb, cb);
-    if (do_win) layer_tiles(r, lcdc, sw, pyw, idw, cw);
-  }
-  const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
-  // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
-  const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
-                        (((bgp >> 6) & 3u) << 24)) & bg_on;
-  // Output words are staged over the wavefront's own line buffer: word g of
-  // lane l goes to dword g*64 + (l ^ g), inside the first 256 bytes of group
-  // g/2's entries, which every lane has read by then; the XOR spreads the
-  // column reads of the store phase over the banks.
-  uint32_t* stage = reinterpret_cast<uint32_t*>(&line[0][0][0]);
-  uint32_t pword = 0;
-#pragma unroll
-  for (int g = 0; g < kGroups; ++g) {
-    // colours of samples 4g..4g+3, one per byte
-    uint32_t col = __builtin_amdgcn_alignbyte(cb[g + 1], cb[g], qb);
-    if (win) {
-      // samples x = 8g + 2i >= WX - 7 show the window
-      const int d = min(max((wx7 + 1 - 8 * g) >> 1, 0), 4);
-      const uint32_t m = d >= 4 ? 0u : (~0u << (8 * d));
-      col = (col & ~m) | (__builtin_amdgcn_alignbyte(cw[g + 1], cw[g], qw) & m);
+    for (int j = 0; j < kTileSlots; ++j) cb[j] = cw[j] = 0;
+    if (bg_on) {
+      // the background unless the window covers the whole row
+      const bool do_bg = !(win && wx7 <= 0), do_win = win && wx7 < 2 * kDsW - 1;
+      const uint32_t pyb = (y + scy) & 0xFFu, pyw = (y - wy) & 0xFFu;
+      // one layer after the other (from LDS the reads need no batching
+      // across layers, and the tile ids of one layer fewer hold registers)
+      uint32_t id[kTileSlots];
+      if (do_bg) {
+        layer_ids(r, (lcdc & 0x08u) ? 0x9C00u : 0x9800u, scx, pyb, id);
+        layer_tiles(r, lcdc, scx, pyb, id, cb);
+      }
+      if (do_win) {
+        layer_ids(r, (lcdc & 0x40u) ? 0x9C00u : 0x9800u, sw, pyw, id);
+        layer_tiles(r, lcdc, sw, pyw, id, cw);
+      }
     }
-    col &= bg_on;
-    uint32_t shade = __builtin_amdgcn_perm(0u, pbg, col);
-    const uint2 ob = *reinterpret_cast<const uint2*>(&line[g][lane][0]);
-    const uint32_t w = __builtin_amdgcn_perm(ob.y, ob.x, 0x06040200u);  // low byte of each entry
-    const uint32_t nz = (col | (col >> 1)) & 0x01010101u;
-    const uint32_t show = (w >> 3) & ~((w >> 2) & nz) & 0x01010101u;
-    const uint32_t sm = (show << 8) - show;
-    shade = (sm & w & 0x03030303u) | (~sm & shade);
-    if (packed) {
+    if (more) fetch(nblk_next, npart, KH{}, KN{});
+    const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
+    // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
+    const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
+                          (((bgp >> 6) & 3u) << 24)) & bg_on;
+    uint32_t word[kGroups] = {};
+    uint32_t pword = 0;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      // colours of samples 4g..4g+3, one per byte
+      uint32_t col = __builtin_amdgcn_alignbyte(cb[g + 1], cb[g], qb);
+      if (win) {
+        // samples x = 8g + 2i >= WX - 7 show the window
+        const int d = min(max((wx7 + 1 - 8 * g) >> 1, 0), 4);
+        const uint32_t m = d >= 4 ? 0u : (~0u << (8 * d));
+        col = (col & ~m) | (__builtin_amdgcn_alignbyte(cw[g + 1], cw[g], qw) & m);
+      }
+      col &= bg_on;
+      uint32_t shade = __builtin_amdgcn_perm(0u, pbg, col);
+      const uint2 ob = *reinterpret_cast<const uint2*>(&obj[g][tid][0]);
+      const uint32_t w = __builtin_amdgcn_perm(ob.y, ob.x, 0x06040200u);  // low byte of each entry
+      const uint32_t nz = (col | (col >> 1)) & 0x01010101u;
+      const uint32_t show = (w >> 3) & ~((w >> 2) & nz) & 0x01010101u;
+      const uint32_t sm = (show << 8) - show;
+      shade = (sm & w & 0x03030303u) | (~sm & shade);
       // shades s0..s3 to s0 | s1 << 2 | s2 << 4 | s3 << 6 (no overlapping terms)
       pword |= ((shade * 0x01041040u) >> 24) << (8 * (g & 3));
       if ((g & 3) == 3) {
-        stage[(g >> 2) * kEnvBlock + (lane ^ (uint32_t)(g >> 2))] = pword;
+        if (packed) word[g >> 2] = pword;
         pword = 0;
       }
-    } else {
-      stage[g * kEnvBlock + (lane ^ (uint32_t)g)] = shade;
+      if (!packed) word[g] = shade;
     }
+    // The stage: per wavefront (8 output rows of the 8 envs) its words in
+    // output order, env by env, row by row.
+    __syncthreads();
+    const uint32_t wave = tid >> 6, lane = tid & 63u, r8 = oy & 7u;
+    uint32_t* stage = reinterpret_cast<uint32_t*>(&obj[0][0][0]);
+    constexpr uint32_t nw = packed ? (uint32_t)kDsWB / 4u : (uint32_t)kGroups;  // words per row
+    uint32_t* mine = stage + wave * 64u * nw + (env * 8u + r8) * nw;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g)
+      if ((uint32_t)g < nw) mine[g] = word[g];
+    __syncthreads();
+    constexpr size_t env_bytes = (size_t)nw * 4u * kDsH;
+    const uint32_t env0 = blk * (uint32_t)kEnvBlock + part * (uint32_t)kImgEnvs;
+    // The wavefront's words in output order: env e's 8 rows are 8 * nw
+    // consecutive words of its output, from byte wave * 32 * nw on.
+    const uintptr_t ob = (uintptr_t)(out + base);
+    const uint32_t* wst = stage + wave * 64u * nw;
+    if ((ob & 15u) == 0u) {
+      // 16 bytes per lane (an env's words are a multiple of 4)
+#pragma unroll
+      for (uint32_t d = 4u * lane; d < 64u * nw; d += 256u) {
+        const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
+        if (env0 + e < (uint32_t)s.n)
+          *reinterpret_cast<uint4*>(out + base + (size_t)(env0 + e) * env_bytes + wave * 32u * nw + 4u * w2) =
+              *reinterpret_cast<const uint4*>(wst + d);
+      }
+    } else {
+      const bool aligned = (ob & 3u) == 0u;
+#pragma unroll
+      for (uint32_t d = lane; d < 64u * nw; d += 64u) {
+        const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
+        if (env0 + e < (uint32_t)s.n) {
+          const uint32_t wd = wst[d];
+          uint8_t* p = out + base + (size_t)(env0 + e) * env_bytes + wave * 32u * nw + 4u * w2;
+          if (aligned) {
+            *reinterpret_cast<uint32_t*>(p) = wd;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) p[q] = (uint8_t)(wd >> (8 * q));
+          }
+        }
+      }
+    }
+    // every wavefront is done with the image and the stage
+    __syncthreads();
+    blk = nblk_next;
+    part = npart;
   }
-  __syncthreads();
-  uint8_t* rows = out + base + ((size_t)blk * kEnvBlock * kDsH + oy) * (packed ? kDsWB : kDsW);
-  const bool aligned = (((uintptr_t)(out + base)) & 3u) == 0;
-  if (packed)
-    store_rows<kDsWB / 4>(stage, rows, (size_t)kDsWB * kDsH, blk, lane, (uint32_t)s.n, aligned);
-  else
-    store_rows<kDsW / 4>(stage, rows, (size_t)kDsW * kDsH, blk, lane, (uint32_t)s.n, aligned);
 }
 
 // ---------------------------------------------------------------------------
@@ -670,8 +769,29 @@ hipError_t launch_render_bg_env0(const DevState& s, uint8_t* out, hipStream_t st
 hipError_t launch_render(const DevState& s, uint8_t* out, int64_t base, int packed,
                          hipStream_t st) {
   if (s.n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(render_kernel, dim3((unsigned)(s.npad / kEnvBlock), kDsH / kRenderRows),
-                     dim3(kRenderThreads), 0, st, s, out, base, packed);
+  // One workgroup fills a CU's LDS: with the blocks a multiple of 8 and the
+  // groups spread evenly, one workgroup per CU (rounded down to a multiple
+  // of 64) renders several groups, loading each next image while it renders
+  // the current one; otherwise one group per workgroup.
+  const uint32_t groups = (uint32_t)(s.npad / kImgEnvs);
+  int dev = 0, cus = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess) return err;
+  uint32_t wgs = groups, rounds = 1;
+  if (((s.npad >> kEnvBlockShift) & 7) == 0) {
+    for (uint32_t w = ((uint32_t)cus / 64u) * 64u; w >= 64u; w -= 64u) {
+      if (groups % w == 0 && groups / w >= 2u) {
+        wgs = w;
+        rounds = groups / w;
+        break;
+      }
+    }
+  }
+  if (packed)
+    hipLaunchKernelGGL(render_kernel<true>, dim3(wgs), dim3(kImgThreads), 0, st, s, out, base, rounds);
+  else
+    hipLaunchKernelGGL(render_kernel<false>, dim3(wgs), dim3(kImgThreads), 0, st, s, out, base, rounds);
   return hipGetLastError();
 }
 

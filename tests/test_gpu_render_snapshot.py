@@ -4,7 +4,10 @@ Every env gets its own random VRAM, OAM and LCDC/scroll/window/palette
 registers (8x8 and 8x16 sprites, both tile-data and tile-map selects, window
 on and off, BG and sprites each enabled or not), with sprites crowded onto a
 few lines so the 10-per-line limit, x-priority ties and BG-over-OBJ all come
-up; the packed and unpacked outputs must equal the oracle's bytes.
+up; the packed and unpacked outputs must equal the oracle's bytes.  The
+larger env counts are rendered by workgroups that each take several groups
+of envs in turn (one workgroup per CU), 4,056 with padding envs in its last
+block.
 """
 
 from __future__ import annotations
@@ -34,7 +37,7 @@ def _scene(rng: np.random.Generator) -> dict[int, bytes]:
     return {0x8000: vram.tobytes(), 0xFE00: oam.tobytes(), 0xFF40: io.tobytes()}
 
 
-@pytest.mark.parametrize("n,seed", [(200, 5), (64, 6), (256, 7)])
+@pytest.mark.parametrize("n,seed", [(200, 5), (64, 6), (256, 7), (4056, 8), (8192, 9)])
 def test_snapshot_render_random_scenes(carts, bootstub, n, seed):
     require_gpu()
     import torch
@@ -57,11 +60,12 @@ def test_snapshot_render_random_scenes(carts, bootstub, n, seed):
         dut.render_pixels_snapshot()
         ref.render(packed=False, threads=8)
         np.testing.assert_array_equal(dut.pixels_torch().cpu().numpy(), ref.pix)
-        out = torch.zeros(n * 72 * 20 + 3, dtype=torch.uint8, device="cuda")
-        dut.render_pixels_snapshot_packed_to_torch(out, 3)  # unaligned rows
         ref.render(packed=True, threads=8)
-        got = out[3:].cpu().numpy().reshape(n, 72, 20)
-        np.testing.assert_array_equal(got, ref.pix_packed)
+        for off in (3, 4, 16):  # rows at byte, word and 16-byte alignment
+            out = torch.zeros(n * 72 * 20 + off, dtype=torch.uint8, device="cuda")
+            dut.render_pixels_snapshot_packed_to_torch(out, off)
+            got = out[off:].cpu().numpy().reshape(n, 72, 20)
+            np.testing.assert_array_equal(got, ref.pix_packed)
         assert np.unique(ref.pix).size == 4
     finally:
         dut.close()
