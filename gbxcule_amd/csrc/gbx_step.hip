@@ -277,7 +277,7 @@ struct Lane {
     const uint32_t win = (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
     const uint32_t roff = win + ((rom_len + x - win) & (0u - (uint32_t)bootw));
     // (a ROM-only cart without RAM never has ram_ok: its offset folds away)
-    const uint32_t coff = ((mbc == MBC_ROM_ONLY) & !cram) | !ram_ok
+    const uint32_t coff = (((mbc == MBC_ROM_ONLY) & !cram) | !ram_ok)
                               ? lane
                               : ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane;
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
