@@ -1230,6 +1230,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
     const uint32_t lcdc_prev = L.lcdc & 0x80u;
     const bool hiter = L.halted != 0;
     int cycles = 4;
+    // the cycles of a batched step (HALT, poll or copy passes) before its
+    // last 4-cycle halted step or last instruction (a taken JR, 12 cycles):
+    // the RTC counts them before the step's interrupt check, whose push may
+    // write the RTC registers (the reference ticks it after every step)
+    int rtc_pre = 0;
     uint32_t op = 0;
     const uint32_t pc_before = L.pc;
     // pending bus writes: the instruction's, then the interrupt push
@@ -1336,6 +1341,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
               L.w1 = ((hl + (uint32_t)k) << 16) | ((nbc | (nbc >> 8)) & 0xFFu);
               npc = pc;
               cycles = 52 * k;
+              rtc_pre = cycles - 12;
               ninstr += 7u * (uint32_t)k - 1u;
             }
           } else if (!dbg && (o.misc & 16u)) {
@@ -1356,6 +1362,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
               L.w1 = (L.w1 & 0xFFFF0000u) | (f << 8) | ly;
               npc = pc;
               cycles = 32 * k;
+              rtc_pre = cycles - 12;
               ninstr += 3u * (uint32_t)k - 1u;
             }
           }
@@ -1372,6 +1379,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
     } else {
       L.settle();
       cycles = L.halt_cycles(cframe);
+      rtc_pre = cycles - 4;
     }
 
     // ---- write phase, debug checks, timer, PPU, interrupt check --------------
@@ -1422,6 +1430,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
         L.ime_delay = 0;
       }
       uint32_t lcdc_now = L.ppu_advance(cycles);
+      if (kMbc == MBC_MBC3) L.rtc_tick(rtc_pre);
       const uint32_t pending = L.ie & L.ifr & 0x1Fu;
       if (__builtin_expect(pending != 0u, 0)) {
         L.halted = 0;
@@ -1452,7 +1461,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       }
 
       const int total = cycles + svc;
-      L.rtc_tick(total);
+      L.rtc_tick(total - rtc_pre);
       ncyc += (uint32_t)total;
       cframe += total;
       if (__builtin_expect((((lcdc_prev ^ lcdc_now) & 0x80u) != 0u) | (cframe >= kCyclesPerFrame), 0)) {
