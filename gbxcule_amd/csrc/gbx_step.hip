@@ -99,6 +99,12 @@ struct Ref32 {
 };
 
 __device__ __forceinline__ uint32_t sel(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
+// c ? a : b for two computed addresses, marked unpredictable: left to
+// itself the compiler may turn such a select into a branch around the
+// computation of one address, which then sits in front of the load.
+__device__ __forceinline__ const uint8_t* sel_ptr(bool c, const uint8_t* a, const uint8_t* b) {
+  return __builtin_unpredictable(c) ? a : b;
+}
 // Lane q's value of v, unsigned (the builtin returns int, which would
 // sign-extend when widened).
 __device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t q) {
@@ -129,6 +135,9 @@ template <typename T>
 __device__ __forceinline__ T ld_global(const T* p) {
   return *(const __attribute__((address_space(1))) T*)p;
 }
+__device__ __forceinline__ void st_global(const uint8_t* p, uint32_t v) {
+  *(__attribute__((address_space(1))) uint8_t*)const_cast<uint8_t*>(p) = (uint8_t)v;
+}
 
 // ---------------------------------------------------------------------------
 // Per-lane machine.  Everything here is scalarized into VGPRs.
@@ -136,7 +145,7 @@ __device__ __forceinline__ T ld_global(const T* p) {
 struct Lane {
   const DevState& s;
   int mbc;        // cartridge kind; a compile-time constant of each kernel variant
-  bool cram;      // the cart declares RAM; compile-time too (ROM-only carts may)
+  bool cram;      // the cart declares RAM; compile-time too (false: ram_ok never holds)
   uint32_t e;     // env index
   uint32_t lane;  // e % 64: position inside the 64-env block
   rsrc_t rm, rsc, rcs;             // memory image, scalars, cartridge state of the block
@@ -175,8 +184,20 @@ struct Lane {
   // cartridge
   uint32_t boot_en;
   uint32_t rom_lo, rom_hi;  // byte offset of the 0000 / 4000 windows in the ROM buffer
-  uint32_t ram_ok, ram_off;
+  // MBC registers as the step uses them, packed into one word (the
+  // cartridge state keeps each value as written): ROM bank bits 0-6, upper
+  // bank bits 8-9, banking mode bit 10, RAM enable bit 11, RTC select bits
+  // 12-15, RAM bank bits 16-17, RTC latch bit 18.
+  uint32_t mbr;
+  uint32_t ram_ok;
   int rtc_field;       // 0..4 when an RTC register is mapped at A000
+  // The byte the bus reads at A000 (cart_p) and the mask of the row offset
+  // of an A000-BFFF address (cart_m): ~0 while a RAM bank is mapped; 0 while
+  // an RTC register is (every address reads the low byte of its cartridge
+  // state slot) or nothing is (the byte read is replaced by 0xFF, so any
+  // in-bounds byte serves: the env's byte of cartridge RAM row 0).
+  const uint8_t* cart_p;
+  uint32_t cart_m;
   int rtc_sub;
   uint32_t rtc_halt, rtc_dirty;
   uint32_t map_changed;  // set when a write remaps the fetch windows
@@ -215,11 +236,23 @@ struct Lane {
     if (mask >= 0) return bank & mask;
     return bank % count;
   }
+  static constexpr uint32_t kMbrEn = 1u << 11, kMbrLatch = 1u << 18;
+  // mbr from the cartridge state slots, masked as the bus uses them
+  __device__ uint32_t load_mbr() const {
+    uint32_t m = CS(CS_RAM_ENABLE) != 0 ? kMbrEn : 0u;
+    if (mbc != MBC_ROM_ONLY) {
+      m |= ((uint32_t)CS(CS_ROM_BANK_LO) & 0x7Fu) | (((uint32_t)CS(CS_ROM_BANK_HI) & 3u) << 8) |
+           (((uint32_t)CS(CS_BANK_MODE) & 1u) << 10) | (((uint32_t)CS(CS_RAM_BANK) & 3u) << 16);
+      if (mbc == MBC_MBC3)
+        m |= (((uint32_t)CS(CS_RTC_SELECT) & 0xFu) << 12) | (CS(CS_RTC_LATCH) != 0 ? kMbrLatch : 0u);
+    }
+    return m;
+  }
   __device__ void refresh_cart() {
     const int kind = mbc;
-    const int lo_raw = CS(CS_ROM_BANK_LO);
-    const int lo = lo_raw & 0x1F, hi = CS(CS_ROM_BANK_HI) & 3;
-    const int mode = CS(CS_BANK_MODE) & 1;
+    const int lo_raw = (int)(mbr & 0x7Fu);
+    const int lo = lo_raw & 0x1F, hi = (int)((mbr >> 8) & 3u);
+    const int mode = (int)((mbr >> 10) & 1u);
     int b0 = (kind == MBC_MBC1 && mode) ? (hi & 3) << 5 : 0;
     int b1;
     if (kind == MBC_ROM_ONLY) {
@@ -238,20 +271,33 @@ struct Lane {
     const uint32_t open = rom_len + 0x100u;
     rom_lo = ((int64_t)b0 * 0x4000 < lim) ? (uint32_t)b0 * 0x4000u : open;
     rom_hi = ((int64_t)b1 * 0x4000 < lim) ? (uint32_t)b1 * 0x4000u : open;
-    ram_ok = (s.ram_banks > 0 && CS(CS_RAM_ENABLE) != 0) ? 1u : 0u;
+    // (a runtime value even where cram rules RAM out: folded to a constant
+    // it changed the compiler's schedule of the bus read, 1.7% slower)
+    ram_ok = ((s.ram_banks > 0) & ((mbr & kMbrEn) != 0u)) ? 1u : 0u;
     rtc_field = -1;
     if (kind == MBC_MBC3) {
-      const int sl = CS(CS_RTC_SELECT) & 0x0F;
+      const int sl = (int)((mbr >> 12) & 0xFu);
       if (sl >= 0x08 && sl <= 0x0C) rtc_field = sl - 0x08;
     }
     int rb = 0;
     if (kind == MBC_MBC1) {
-      if (mode) rb = CS(CS_RAM_BANK) & 3;
+      if (mode) rb = (int)((mbr >> 16) & 3u);
     } else if (kind == MBC_MBC3) {
-      rb = CS(CS_RAM_BANK) & 3;
+      rb = (int)((mbr >> 16) & 3u);
     }
     rb = clamp_bank(rb, s.ram_banks, -1);
-    ram_off = (uint32_t)rb * 0x2000u;
+    const size_t blk = e >> kEnvBlockShift;
+    const uint8_t* cb = cramb;
+    cart_p = cb + lane;
+    cart_m = 0u;
+    if (ram_ok && rtc_field >= 0) {
+      const uint32_t slot = (uint32_t)(((mbr & kMbrLatch) ? CS_RTC_L_SECONDS : CS_RTC_SECONDS) + rtc_field);
+      cart_p = reinterpret_cast<const uint8_t*>(s.cs + blk * (kCartStateStride * kEnvBlock)) +
+               (((slot << kEnvBlockShift) | lane) << 2);
+    } else if (ram_ok) {
+      cart_p = cb + ((((uint32_t)rb * 0x2000u) << kEnvBlockShift) | lane);
+      cart_m = ~0u;
+    }
   }
 
   // -- bus read (reference read8, cpu_step_builder.py:538-657) ----------------
@@ -265,9 +311,9 @@ struct Lane {
   }
   __device__ static bool io_derived(uint32_t x) { return (x & 0xFFBAu) == 0xFF00u; }
   // Flat address of the byte the bus returns at x (echo-folded): ROM window,
-  // boot image, or the 0xFF filler for an unmapped bank; cartridge RAM; or
-  // the env's memory.  Disabled cartridge RAM and the RTC registers are
-  // resolved by cart_fix.
+  // boot image, or the 0xFF filler for an unmapped bank; cartridge RAM or
+  // the mapped RTC register; or the env's memory.  Disabled cartridge RAM is
+  // resolved by bus_fix.
   __device__ const uint8_t* bus_ptr(uint32_t x) const {
     const bool rom = x < 0x8000u;
     const bool cart = x - 0xA000u < 0x2000u;
@@ -276,35 +322,21 @@ struct Lane {
     const bool bootw = (boot_en != 0u) & (x < 0x100u);
     const uint32_t win = (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
     const uint32_t roff = win + ((rom_len + x - win) & (0u - (uint32_t)bootw));
-    // (a ROM-only cart without RAM never has ram_ok: its offset folds away)
-    const uint32_t coff = (((mbc == MBC_ROM_ONLY) & !cram) | !ram_ok)
-                              ? lane
-                              : ((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane;
+    // (a cart without RAM never maps any: the byte read is the env's byte of
+    // cartridge RAM row 0, replaced by 0xFF)
+    const uint8_t* cp = cram ? cart_p + (((x - 0xA000u) << kEnvBlockShift) & cart_m) : cramb + lane;
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
-    p = cart ? cramb + coff : p;
-    p = rom ? this->rom + roff : p;
-    return p;
+    p = cart ? cp : p;
+    return sel_ptr(rom, this->rom + roff, p);
   }
   __device__ static uint32_t fold(uint32_t addr) {
     const uint32_t x = addr & 0xFFFFu;
     return x - 0xE000u < 0x1E00u ? x - 0x2000u : x;
   }
-  __device__ uint32_t rtc_read() const {
-    const bool latched = CS(CS_RTC_LATCH) != 0;
-    return (uint32_t)CS((latched ? CS_RTC_L_SECONDS : CS_RTC_SECONDS) + rtc_field) & 0xFFu;
-  }
-  __device__ uint32_t cart_fix(uint32_t v) const {
-    if (!ram_ok) return 0xFFu;
-    return rtc_field >= 0 ? rtc_read() : v;
-  }
   // Value the bus returned for a load v issued at bus_ptr(x).
   __device__ uint32_t bus_fix(uint32_t x, uint32_t v) const {
     const bool cart = x - 0xA000u < 0x2000u;
-    if (mbc == MBC_MBC3) {
-      if (cart) v = cart_fix(v);
-    } else {
-      v = (cart & !ram_ok) ? 0xFFu : v;  // no RTC: disabled RAM reads 0xFF
-    }
+    v = (cart & !ram_ok) ? 0xFFu : v;  // disabled or absent cartridge RAM reads 0xFF
     // DIV and STAT, which follow from the timer and PPU position, and TIMA and
     // LY while edges and scanline changes are deferred (FF05 and FF44 hold
     // the values of the last applied ones): FF04 FF05 FF40 FF41 FF44 FF45
@@ -553,35 +585,56 @@ struct Lane {
     }
     tdiv = div;  // a DIV or TAC write starts the count afresh
   }
+  // The slots a write changes are stored as the reference stores them, and
+  // mbr follows, so that refresh_cart reads no memory.
   __device__ void mbc_write(uint32_t x, uint32_t v) {
     const int kind = mbc;
-    if (kind == MBC_MBC1) {
-      if (x < 0x2000u) CS(CS_RAM_ENABLE) = (v & 0x0Fu) == 0x0Au ? 1 : 0;
-      else if (x < 0x4000u) CS(CS_ROM_BANK_LO) = (v & 0x1Fu) ? (int)(v & 0x1Fu) : 1;
-      else if (x < 0x6000u) {
-        CS(CS_ROM_BANK_HI) = (int)(v & 3u);
-        CS(CS_RAM_BANK) = (int)(v & 3u);
+    if (kind == MBC_ROM_ONLY) return;
+    const uint32_t lo_bits = kind == MBC_MBC1 ? 0x1Fu : 0x7Fu;
+    if (x < 0x2000u) {
+      const uint32_t en = (v & 0x0Fu) == 0x0Au ? 1u : 0u;
+      CS(CS_RAM_ENABLE) = (int)en;
+      mbr = (mbr & ~kMbrEn) | (en << 11);
+    } else if (x < 0x4000u) {
+      const uint32_t b = (v & lo_bits) ? (v & lo_bits) : 1u;
+      CS(CS_ROM_BANK_LO) = (int)b;
+      mbr = (mbr & ~0x7Fu) | b;
+    } else if (kind == MBC_MBC1) {
+      if (x < 0x6000u) {
+        const uint32_t h = v & 3u;
+        CS(CS_ROM_BANK_HI) = (int)h;
+        CS(CS_RAM_BANK) = (int)h;
+        mbr = (mbr & ~0x30300u) | (h << 8) | (h << 16);
       } else {
         CS(CS_BANK_MODE) = (int)(v & 1u);
+        mbr = (mbr & ~(1u << 10)) | ((v & 1u) << 10);
       }
-    } else if (kind == MBC_MBC3) {
-      if (x < 0x2000u) CS(CS_RAM_ENABLE) = (v & 0x0Fu) == 0x0Au ? 1 : 0;
-      else if (x < 0x4000u) CS(CS_ROM_BANK_LO) = (v & 0x7Fu) ? (int)(v & 0x7Fu) : 1;
-      else if (x < 0x6000u) {
-        const int sl = (int)(v & 0x0Fu);
-        CS(CS_RTC_SELECT) = sl;
-        if (sl <= 3) CS(CS_RAM_BANK) = sl;
-      } else if (v == 0) {
-        CS(CS_RTC_LATCH) = 0;
-      } else if (v == 1 && CS(CS_RTC_LATCH) == 0) {
-        for (int k = 0; k < 5; ++k) CS(CS_RTC_L_SECONDS + k) = CS(CS_RTC_SECONDS + k);
-        CS(CS_RTC_LATCH) = 1;
+    } else if (x < 0x6000u) {
+      const uint32_t sl = v & 0x0Fu;
+      CS(CS_RTC_SELECT) = (int)sl;
+      mbr = (mbr & ~0xF000u) | (sl << 12);
+      if (sl <= 3u) {
+        CS(CS_RAM_BANK) = (int)sl;
+        mbr = (mbr & ~0x30000u) | (sl << 16);
       }
-    } else {
-      return;
+    } else if (v == 0) {
+      CS(CS_RTC_LATCH) = 0;
+      mbr &= ~kMbrLatch;
+    } else if ((v == 1) & ((mbr & kMbrLatch) == 0u)) {
+      int r[5];
+      for (int k = 0; k < 5; ++k) r[k] = CS(CS_RTC_SECONDS + k);
+      for (int k = 0; k < 5; ++k) CS(CS_RTC_L_SECONDS + k) = r[k];
+      CS(CS_RTC_LATCH) = 1;
+      mbr |= kMbrLatch;
     }
+    const uint32_t lo0 = rom_lo, hi0 = rom_hi;
     refresh_cart();
-    map_changed = 1;  // write_bus drops the prefetched record
+    // write_bus drops the prefetched record only when a fetch window moved:
+    // RAM enable, RAM bank, RTC select and latch writes, and bank writes of
+    // the bank already mapped, leave every record index as it was.  (Sticky:
+    // the first byte of a two-byte write may move a window the second byte
+    // leaves alone.)
+    map_changed |= ((rom_lo != lo0) | (rom_hi != hi0)) ? 1u : 0u;
   }
   __device__ void write_special(uint32_t x, uint32_t v) {
     if (x < 0x8000u) {
@@ -595,10 +648,7 @@ struct Lane {
         if (rtc_field == 4) rtc_halt = (v & 0x40u) ? 1u : 0u;
         return;
       }
-      __builtin_amdgcn_raw_buffer_store_b8(
-          (uint8_t)v,
-          make_rsrc(cramb, (uint32_t)s.cram_stride * kEnvBlock),
-          (int)(((ram_off + (x - 0xA000u)) << kEnvBlockShift) | lane), 0, 0);
+      st_global(cart_p + ((x - 0xA000u) << kEnvBlockShift), v);  // a RAM bank is mapped
     } else {
       io_write(x, v);
     }
@@ -631,10 +681,18 @@ struct Lane {
   // stores its first byte twice.  An MBC bank write clears rv, the validity
   // of the record already fetched for the next pc (the boot ROM switch is an
   // IO write, after which the full sequence drops the record).
+  // With cartridge RAM (cram), a byte of a mapped RAM bank is a plain store
+  // too, into the cartridge RAM buffer instead of the env's memory.
+  __device__ bool cart_plain(uint32_t x) const { return cram & (x - 0xA000u < 0x2000u) & (cart_m != 0u); }
+  __device__ uint8_t* store_ptr(uint32_t x, bool c) const {
+    return const_cast<uint8_t*>(c ? cart_p + ((x - 0xA000u) << kEnvBlockShift)
+                                  : memb + ((x << kEnvBlockShift) | lane));
+  }
   __device__ void write_bus(uint32_t n, uint32_t a0, uint32_t v0, uint32_t a1, uint32_t v1, bool& rv) {
     const uint32_t x0 = a0 & 0xFFFFu, x1 = a1 & 0xFFFFu;
     const bool two = n >= 2u;
-    if (__builtin_expect((!plain_store(x0)) | (two & !plain_ram(x1)), 0)) {
+    const bool c0 = cart_plain(x0), c1 = cart_plain(x1);
+    if (__builtin_expect((!(plain_store(x0) | c0)) | (two & !(plain_ram(x1) | c1)), 0)) {
       write8(a0, v0);
       if (two) write8(a1, v1);
       if (mbc != MBC_ROM_ONLY) {
@@ -645,8 +703,14 @@ struct Lane {
       const bool j0 = x0 == 0xFF00u;
       const uint32_t s0 = j0 ? joyp_read(v0) : v0;
       joyp_sel = j0 ? v0 & 0x30u : joyp_sel;
-      M(x0) = s0;
-      M(two ? x1 : x0) = two ? v1 : s0;
+      if (!cram) {
+        M(x0) = s0;
+        M(two ? x1 : x0) = two ? v1 : s0;
+      } else {
+        uint8_t* p0 = store_ptr(x0, c0);
+        st_global(p0, s0);
+        st_global(two ? store_ptr(x1, c1) : p0, two ? v1 : s0);
+      }
     }
   }
 
@@ -1065,9 +1129,12 @@ struct Lane {
 // ---------------------------------------------------------------------------
 // One variant per cartridge kind (kMbc), per debug mode (kDbg) and, for
 // ROM-only carts, per declared RAM (kCram): the cartridge code of other
-// kinds and every debug check compile out.
+// kinds and every debug check compile out.  The variants for MBC carts
+// with RAM are built for two wavefronts per SIMD (256 VGPRs): at three they
+// spill VGPRs to scratch in the loop, and 131,072 envs in 64-lane
+// wavefronts are two per SIMD.
 template <int kMbc, bool kDbg, bool kCram = true>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void step_kernel(DevState s, StepArgs args) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MBC_ROM_ONLY && kCram) ? 2 : 3))) void step_kernel(DevState s, StepArgs args) {
   const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (uint32_t)s.n) return;
   Lane L{s};
@@ -1131,6 +1198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   L.rtc_dirty = 1;  // first tick of a launch normalizes like the reference does
   L.map_changed = 0;
   L.budget = 0;
+  L.mbr = L.load_mbr();
   L.refresh_cart();
   L.action = args.actions[e];
   L.release = (int)in_vgpr((uint32_t)args.release);
@@ -1609,9 +1677,17 @@ hipError_t launch_step(const DevState& s, const StepArgs& a, hipStream_t st) {
       if (rom_ram) hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, true, true>), g, b, 0, st, s, a);
       else hipLaunchKernelGGL((step_kernel<MBC_ROM_ONLY, true, false>), g, b, 0, st, s, a);
       break;
-    case MBC_MBC1 * 2: hipLaunchKernelGGL((step_kernel<MBC_MBC1, false>), g, b, 0, st, s, a); break;
+    // (an MBC cart without RAM gets the variant whose store path has no
+    // cartridge RAM; the debug variants keep the general one)
+    case MBC_MBC1 * 2:
+      if (s.ram_banks > 0) hipLaunchKernelGGL((step_kernel<MBC_MBC1, false, true>), g, b, 0, st, s, a);
+      else hipLaunchKernelGGL((step_kernel<MBC_MBC1, false, false>), g, b, 0, st, s, a);
+      break;
     case MBC_MBC1 * 2 + 1: hipLaunchKernelGGL((step_kernel<MBC_MBC1, true>), g, b, 0, st, s, a); break;
-    case MBC_MBC3 * 2: hipLaunchKernelGGL((step_kernel<MBC_MBC3, false>), g, b, 0, st, s, a); break;
+    case MBC_MBC3 * 2:
+      if (s.ram_banks > 0) hipLaunchKernelGGL((step_kernel<MBC_MBC3, false, true>), g, b, 0, st, s, a);
+      else hipLaunchKernelGGL((step_kernel<MBC_MBC3, false, false>), g, b, 0, st, s, a);
+      break;
     default: hipLaunchKernelGGL((step_kernel<MBC_MBC3, true>), g, b, 0, st, s, a); break;
   }
   return hipGetLastError();

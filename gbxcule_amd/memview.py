@@ -19,12 +19,15 @@ dtype and device without storage of its own:
   the index is strided or a list of positions);
 * every other operation runs on an env-major copy of all memory (in-place
   operations write it back): correct, but it moves N x 64 KiB each time.
+  Above 1 GiB (16,384 envs) the view warns once (``FullCopyWarning``) and
+  names the indexed forms and ``memory_blocks_torch()``.
 
 All launches go to torch's current stream, in program order.
 """
 
 from __future__ import annotations
 
+import warnings
 from typing import Any, Callable
 
 import numpy as np
@@ -50,6 +53,14 @@ _INPLACE_DUNDER = frozenset(
     ("__iadd__", "__isub__", "__imul__", "__iand__", "__ior__", "__ixor__", "__ilshift__",
      "__irshift__", "__itruediv__", "__ifloordiv__", "__imod__")
 )  # fmt: skip
+
+
+# A full env-major copy larger than this warns once per view.
+FULL_COPY_WARN_BYTES = 1 << 30
+
+
+class FullCopyWarning(UserWarning):
+    """An operation on an ``EnvMemoryView`` copied all of emulated memory."""
 
 
 def _is_inplace(name: str) -> bool:
@@ -140,6 +151,16 @@ class EnvMemoryView(torch.Tensor):
     # -- the three access paths ------------------------------------------------
     def _dense(self) -> torch.Tensor:
         """Env-major copy of all memory, ``[num_envs, 65536]``."""
+        nbytes = self.num_envs * MEM_SIZE
+        if nbytes > FULL_COPY_WARN_BYTES and not getattr(self, "_warned", False):
+            self._warned = True
+            warnings.warn(
+                f"an operation on memory_torch() copied all emulated memory ({nbytes / 2**30:.1f} GiB, "
+                "and writes it back if in place); index the view (mem[:, ADDR], mem[:, lo:hi], "
+                "mem[env, lo:hi]) or use ram_senses_torch() / memory_blocks_torch() to avoid it",
+                FullCopyWarning,
+                stacklevel=4,
+            )
         return self._read_rect(0, self.num_envs, 0, MEM_SIZE)
 
     def _getitem(self, key: Any) -> torch.Tensor:

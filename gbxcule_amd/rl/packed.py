@@ -77,13 +77,26 @@ def packed_l1_distance(packed_obs, packed_goal):
     for name, t in (("packed_obs", packed_obs), ("packed_goal", packed_goal)):
         if t.dtype is not torch.uint8:
             raise ValueError(f"{name}: expected uint8 packed frames, got {t.dtype}")
-    # the goal is one frame: [H, W_bytes] with an optional channel and batch of 1
-    goal = packed_goal.reshape(1, 1, *packed_goal.shape[-2:]) if packed_goal.ndim in (2, 3, 4) else None
-    if packed_obs.ndim != 4 or packed_obs.shape[1] != 1:
+    if packed_obs.ndim != 4:
         raise ValueError(f"packed_obs: expected [N, 1, H, W_bytes], got {tuple(packed_obs.shape)}")
-    if goal is None or goal.numel() != packed_goal.numel() or goal.shape[2:] != packed_obs.shape[2:]:
+    # one goal for every env ([1, H, W_bytes] or [1, 1, H, W_bytes]) or one
+    # per env ([N, 1, H, W_bytes]), as the reference accepts them
+    goal = packed_goal.unsqueeze(0) if packed_goal.ndim == 3 else packed_goal
+    if goal.ndim != 4:
         raise ValueError(
-            f"packed_goal: expected one {tuple(packed_obs.shape[2:])} frame, got {tuple(packed_goal.shape)}"
+            f"packed_goal: expected [1, 1, H, W_bytes], [N, 1, H, W_bytes] or [1, H, W_bytes], "
+            f"got {tuple(packed_goal.shape)}"
+        )
+    if goal.shape[1] != 1:
+        raise ValueError(f"packed_goal: expected channel dim 1, got {tuple(packed_goal.shape)}")
+    if goal.shape[2:] != packed_obs.shape[2:]:
+        raise ValueError(
+            f"packed_goal: spatial shape {tuple(goal.shape[2:])} differs from the observations' "
+            f"{tuple(packed_obs.shape[2:])}"
+        )
+    if goal.shape[0] not in (1, packed_obs.shape[0]):
+        raise ValueError(
+            f"packed_goal: {goal.shape[0]} goals for {packed_obs.shape[0]} observations (expected 1 or N)"
         )
     packed_goal = goal
     o = packed_obs.to(torch.int16)

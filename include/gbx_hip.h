@@ -180,12 +180,14 @@ int gbx_export_latches(gbx_ctx* ctx, uint8_t* host_out);
 int gbx_export_env(gbx_ctx* ctx, int32_t env, int64_t* scalars, int32_t* cart_state,
                    uint8_t* mem, uint8_t* cart_ram);
 /* gbx_export_env that allocates nothing: no counterpart in the reference.
- * For callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc).  The env
- * image is staged in a static 128 KiB device array that each GPU holds until
- * the process ends, so carts with more than 32 KiB of cart RAM are rejected
- * (GBX_E_UNSUPPORTED) and calls that overlap on one GPU race.  Same outputs
- * as gbx_export_env; the context's device must be current. */
+ * For callers that cannot allocate device memory (tight serving loops,
+ * harnesses that forbid hipMalloc).  The env image is staged in a static
+ * 128 KiB device array that each GPU holds until the process ends, so carts
+ * with more than 32 KiB of cart RAM are rejected (GBX_E_UNSUPPORTED) and
+ * calls that overlap on one GPU race.  Like gbx_export_env it synchronizes
+ * the device and copies to host memory synchronously, so it is not for use
+ * under stream capture.  Same outputs as gbx_export_env; the context's
+ * device must be current. */
 int gbx_export_env_noalloc(gbx_ctx* ctx, int32_t env, int64_t* scalars,
                            int32_t* cart_state, uint8_t* mem, uint8_t* cart_ram);
 int gbx_import_env(gbx_ctx* ctx, int32_t env, const int64_t* scalars,

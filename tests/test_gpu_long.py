@@ -11,17 +11,19 @@
   frame loop: with the LCD on, cycle_in_frame = LY * 456 + scanline cycle
   (both restart together when the LCD is switched on and advance by the same
   cycles), and cycle_count - cycle_in_frame grows by exactly frameskip *
-  70,224 per step while the LCD is not switched.  C2 runs 200 of its 1,000
-  steps by default (the step kernel takes about 0.2 s per launch);
-  GBX_LONG=1 runs all 1,000.  C5 runs all 2,000: its 256-entry SCX/SCY walk
-  wraps many times.
+  70,224 per step while the LCD is not switched.  C2 runs all 1,000 steps,
+  as five tests of 200 steps that continue one run (about 0.14 s per
+  launch).  C5 runs all 2,000: its 256-entry SCX/SCY walk wraps many times.
+* C3 (16,384 envs, packed render every step) for 240 steps, sampled the
+  same way, the sample's packed observation included.
+* C4 (512 KiB MBC1 cart, timer/VBlank/STAT interrupts, HALT wake loops) at
+  its target shape, 131,072 envs, for 200 steps, sampled the same way.
 * The MBC3 cart (C4's variant, 32 KiB cart RAM, RTC) for 200 steps at 8,192
-  envs: 80 emulated seconds, so the RTC carries into minutes.
+  envs: 80 emulated seconds, so the RTC carries into minutes; every env's
+  clock must equal the closed form of its cycle count.
 """
 
 from __future__ import annotations
-
-import os
 
 import numpy as np
 import pytest
@@ -34,7 +36,7 @@ from .conftest import require_gpu
 
 pytestmark = pytest.mark.gpu
 
-CS_RTC_SECONDS, CS_RTC_MINUTES = 9, 10
+CS_RTC_SECONDS, CS_RTC_MINUTES, CS_RTC_LAST_CYCLE = 9, 10, 14
 
 
 def _backend(rom, boot, n, fs, render):
@@ -101,6 +103,10 @@ def _compare_sample(dut, ref, sample, tag, render=None) -> None:
     np.testing.assert_array_equal(dut.export_serial()[sample], ref.serial_buf, err_msg=f"{tag} serial")
     if render == "unpacked":
         np.testing.assert_array_equal(dut.pixels_torch()[idx].cpu().numpy(), ref.pix, err_msg=f"{tag} pixels")
+    if render == "packed":
+        np.testing.assert_array_equal(
+            dut.pixels_packed_torch()[idx].cpu().numpy(), ref.pix_packed, err_msg=f"{tag} packed pixels"
+        )
 
 
 def test_c1_every_step_of_the_full_trace(carts, bootstub):
@@ -124,31 +130,76 @@ def test_c1_every_step_of_the_full_trace(carts, bootstub):
         ref.close()
 
 
-def test_c2_long_trace(carts, bootstub):
+class SampledRun:
+    """A workload on the GPU at full size with a sample of its envs replayed
+    on the oracle, advanced in parts so that a long trace reports as it
+    goes.  Checkpoints every ``every`` steps: the frame invariants over every
+    env and the sample's full state."""
+
+    def __init__(self, rom, boot, n, fs, seed, tag, every, sample_size=6, render=None):
+        rng = np.random.default_rng(seed)
+        self.sample = np.unique(
+            np.concatenate([[0, n - 1], rng.choice(n, sample_size, replace=False)])
+        ).astype(np.int64)
+        self.n, self.fs, self.seed, self.tag, self.every = n, fs, seed, tag, every
+        self.render = render
+        self.dut = _backend(rom, boot, n, fs, render)
+        self.ref = RefMachine(self.sample.size, rom, boot)
+        self.inv = FrameInvariants(fs)
+        self.k = 0
+        self.dut.reset(seed=seed)
+        self.ref.step(None, 0, 0, "full_step")
+
+    def advance_to(self, steps: int) -> None:
+        while self.k < steps:
+            act = seeded_actions(self.seed, self.k, self.n)
+            _step_async(self.dut, act)
+            self.ref.step(act[self.sample], self.fs, 8, "full_step", threads=8)
+            if self.render:
+                self.ref.render(packed=self.render == "packed", threads=8)
+            self.k += 1
+            if self.k % self.every == 0 or self.k == 1:
+                self.inv.check(self.dut, self.k, self.tag)
+                _compare_sample(self.dut, self.ref, self.sample, f"{self.tag} step {self.k}", self.render)
+
+    def close(self) -> None:
+        self.dut.close()
+        self.ref.close()
+
+
+@pytest.fixture(scope="module")
+def c2_run(carts, bootstub):
     require_gpu()
-    n, fs, seed = 16384, 24, 1
-    steps = 1000 if os.environ.get("GBX_LONG") == "1" else 200
-    every = 50
-    rom = carts["c2"]
-    rng = np.random.default_rng(seed)
-    sample = np.unique(np.concatenate([[0, n - 1], rng.choice(n, 6, replace=False)])).astype(np.int64)
-    dut = _backend(rom, bootstub, n, fs, None)
-    ref = RefMachine(sample.size, rom, bootstub)
-    inv = FrameInvariants(fs)
+    run = SampledRun(carts["c2"], bootstub, 16384, 24, 1, "c2-long", every=50)
+    yield run
+    run.close()
+
+
+@pytest.mark.parametrize("part", range(5))
+def test_c2_long_trace(c2_run, part):
+    """C2's 1,000 steps at 16,384 envs, 200 per test."""
+    c2_run.advance_to(200 * (part + 1))
+
+
+def test_c4_mbc1_long_trace_at_target_shape(carts, bootstub):
+    """C4 at 131,072 envs, frameskip 24, 200 steps (4,800 frames)."""
+    require_gpu()
+    run = SampledRun(carts["c4"], bootstub, 131072, 24, 3, "c4-long", every=25, sample_size=8)
     try:
-        dut.reset(seed=seed)
-        ref.step(None, 0, 0, "full_step")
-        for k in range(steps):
-            act = seeded_actions(seed, k, n)
-            _step_async(dut, act)
-            ref.step(act[sample], fs, 8, "full_step", threads=8)
-            if (k + 1) % every == 0 or k == 0:
-                print(f"c2 long trace: step {k + 1}/{steps}", flush=True)
-                inv.check(dut, k + 1, "c2-long")
-                _compare_sample(dut, ref, sample, f"c2-long step {k + 1}")
+        run.advance_to(200)
     finally:
-        dut.close()
-        ref.close()
+        run.close()
+
+
+def test_c3_packed_render_long_trace(carts, bootstub):
+    """C3 at 16,384 envs, frameskip 24, packed 72x80 render every step, 240
+    steps: the SCX/SCY walk table wraps (256 entries, one per frame)."""
+    require_gpu()
+    run = SampledRun(carts["c3"], bootstub, 16384, 24, 2, "c3-long", every=40, render="packed")
+    try:
+        run.advance_to(240)
+    finally:
+        run.close()
 
 
 def test_c5_full_trace_with_restores(carts, bootstub):
@@ -225,6 +276,13 @@ def test_mbc3_rtc_carries_minutes(carts, bootstub):
         cs = dut.export_cart_state()
         assert int(cs[:, CS_RTC_MINUTES].min()) >= 1, "the RTC never carried into minutes"
         assert (cs[sample] == ref.cart_state).all()
+        # nothing writes the clock here: every env's clock is its cycle count
+        # since power-on in whole seconds (4,194,304 cycles), taken apart
+        cyc = dut.export_field("cycle_count").astype(np.int64)
+        secs = cyc // 4194304
+        np.testing.assert_array_equal(cs[:, CS_RTC_SECONDS], secs % 60)
+        np.testing.assert_array_equal(cs[:, CS_RTC_MINUTES], secs // 60 % 60)
+        np.testing.assert_array_equal(cs[:, CS_RTC_LAST_CYCLE], cyc % 4194304)
     finally:
         dut.close()
         ref.close()

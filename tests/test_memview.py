@@ -132,3 +132,29 @@ def test_reference_rl_expressions():
         assert torch.equal(x.float(), store[:, addr].float())
     assert int(v[0, 0xD35E].item()) == int(store[0, 0xD35E])
     np.testing.assert_array_equal(v[0, 0xD747:0xD757].numpy(), store[0, 0xD747:0xD757].numpy())
+
+
+def test_full_copy_warns_once_above_threshold(monkeypatch):
+    """Operations that copy all memory warn once per view when the copy is
+    large; indexing never does."""
+    import warnings
+
+    import gbxcule_amd.memview as mv
+
+    mem, store, _ = _make(3)
+    monkeypatch.setattr(mv, "FULL_COPY_WARN_BYTES", N * 65536 - 1)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        mem[:, 0xD35E]
+        mem[5, 0xC000:0xC010]
+    with pytest.warns(mv.FullCopyWarning):
+        total = mem.sum()
+    assert int(total) == int(store.sum())
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        (mem == 7).any(1)  # second full copy: no second warning
+    monkeypatch.setattr(mv, "FULL_COPY_WARN_BYTES", N * 65536)
+    fresh, _, _ = _make(4)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        fresh.sum()  # at the threshold: no warning

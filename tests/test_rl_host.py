@@ -117,5 +117,14 @@ def test_packed_l1_distance():
         packed_l1_distance(zeros.float(), zeros[0])
     with pytest.raises(ValueError):
         packed_l1_distance(zeros, torch.zeros((1, 72, 19), dtype=torch.uint8))
+    # one goal per env ([N, 1, H, W_bytes]): each env against its own goal
+    goals = torch.randint(0, 256, (6, 1, 72, 20), generator=g, dtype=torch.uint8)
+    per = packed_l1_distance(obs, goals)
+    want = lut[obs.long(), goals.long()].float().sum(dim=(1, 2, 3)) / (72 * 80 * 3)
+    assert torch.equal(per, want)
+    assert torch.equal(packed_l1_distance(obs, goal.unsqueeze(0)), d)  # [1, 1, H, W_bytes]
+    for bad in ((72, 20), (2, 2, 72, 20), (4, 1, 72, 20), (1, 1, 1, 72, 20)):
+        with pytest.raises(ValueError):
+            packed_l1_distance(obs, torch.zeros(bad, dtype=torch.uint8))
     # uniform shades: E|a - b| = 20 / 16 over the 16 pairs, normalised by 3
     assert np.isclose(float(d.mean()), 20 / 16 / 3, atol=0.02)
