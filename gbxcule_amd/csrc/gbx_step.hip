@@ -194,8 +194,9 @@ struct Lane {
   // The byte the bus reads at A000 (cart_p) and the mask of the row offset
   // of an A000-BFFF address (cart_m): ~0 while a RAM bank is mapped; 0 while
   // an RTC register is (every address reads the low byte of its cartridge
-  // state slot) or nothing is (the byte read is replaced by 0xFF, so any
-  // in-bounds byte serves: the env's byte of cartridge RAM row 0).
+  // state slot) or nothing is (every address reads a byte of the 0xFF filler
+  // that follows the boot image in the ROM buffer, which is what disabled or
+  // absent cartridge RAM returns).
   const uint8_t* cart_p;
   uint32_t cart_m;
   int rtc_sub;
@@ -288,7 +289,8 @@ struct Lane {
     rb = clamp_bank(rb, s.ram_banks, -1);
     const size_t blk = e >> kEnvBlockShift;
     const uint8_t* cb = cramb;
-    cart_p = cb + lane;
+    // nothing mapped: a byte of the 0xFF filler after the boot image
+    cart_p = rom + (rom_len + 0x100u);
     cart_m = 0u;
     if (ram_ok && rtc_field >= 0) {
       const uint32_t slot = (uint32_t)(((mbr & kMbrLatch) ? CS_RTC_L_SECONDS : CS_RTC_SECONDS) + rtc_field);
@@ -311,9 +313,9 @@ struct Lane {
   }
   __device__ static bool io_derived(uint32_t x) { return (x & 0xFFBAu) == 0xFF00u; }
   // Flat address of the byte the bus returns at x (echo-folded): ROM window,
-  // boot image, or the 0xFF filler for an unmapped bank; cartridge RAM or
-  // the mapped RTC register; or the env's memory.  Disabled cartridge RAM is
-  // resolved by bus_fix.
+  // boot image, or the 0xFF filler for an unmapped bank; cartridge RAM, the
+  // mapped RTC register, or the 0xFF filler for disabled or absent cartridge
+  // RAM; or the env's memory.
   __device__ const uint8_t* bus_ptr(uint32_t x) const {
     const bool rom = x < 0x8000u;
     const bool cart = x - 0xA000u < 0x2000u;
@@ -322,9 +324,8 @@ struct Lane {
     const bool bootw = (boot_en != 0u) & (x < 0x100u);
     const uint32_t win = (x < 0x4000u ? rom_lo : rom_hi) + (x & 0x3FFFu);
     const uint32_t roff = win + ((rom_len + x - win) & (0u - (uint32_t)bootw));
-    // (a cart without RAM never maps any: the byte read is the env's byte of
-    // cartridge RAM row 0, replaced by 0xFF)
-    const uint8_t* cp = cram ? cart_p + (((x - 0xA000u) << kEnvBlockShift) & cart_m) : cramb + lane;
+    // (a cart without RAM never maps any)
+    const uint8_t* cp = cram ? cart_p + (((x - 0xA000u) << kEnvBlockShift) & cart_m) : this->rom + (rom_len + 0x100u);
     const uint8_t* p = memb + ((x << kEnvBlockShift) | lane);
     p = cart ? cp : p;
     return sel_ptr(rom, this->rom + roff, p);
@@ -333,10 +334,9 @@ struct Lane {
     const uint32_t x = addr & 0xFFFFu;
     return x - 0xE000u < 0x1E00u ? x - 0x2000u : x;
   }
-  // Value the bus returned for a load v issued at bus_ptr(x).
+  // Value the bus returned for a load v issued at bus_ptr(x).  (Disabled or
+  // absent cartridge RAM needs no fix-up: bus_ptr points it at 0xFF.)
   __device__ uint32_t bus_fix(uint32_t x, uint32_t v) const {
-    const bool cart = x - 0xA000u < 0x2000u;
-    v = (cart & !ram_ok) ? 0xFFu : v;  // disabled or absent cartridge RAM reads 0xFF
     // DIV and STAT, which follow from the timer and PPU position, and TIMA and
     // LY while edges and scanline changes are deferred (FF05 and FF44 hold
     // the values of the last applied ones): FF04 FF05 FF40 FF41 FF44 FF45
