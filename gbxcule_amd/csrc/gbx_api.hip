@@ -2,6 +2,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -145,7 +146,8 @@ std::vector<Rec> build_records(const uint8_t* rom, int64_t rom_bytes, const uint
   fill(rom, rom_bytes, 0);
   // LY poll loops and block-copy loops whose bytes lie inside one 16 KiB window
   for (int64_t i = 0; i + 5 < rom_bytes; ++i) {
-    if ((i & 0x3FFF) <= 0x3FFA && poll_loop_at(rom + i)) r[(size_t)i] = mark_poll_loop(r[(size_t)i], rom + i);
+    const uint32_t pl = poll_loop_len(rom + i, (uint32_t)std::min<int64_t>(8, rom_bytes - i));
+    if (pl != 0u && (i & 0x3FFF) + pl <= 0x4000) r[(size_t)i] = mark_poll_loop(r[(size_t)i], rom + i);
     if ((i & 0x3FFF) <= 0x3FF8 && i + 7 < rom_bytes && copy_loop_at(rom + i)) r[(size_t)i] = mark_copy_loop(r[(size_t)i]);
   }
   fill(boot, 0x100, (size_t)rom_bytes);

@@ -448,19 +448,40 @@ __host__ __device__ constexpr Rec pack(Dec d) {
 
 __host__ __device__ constexpr uint32_t sext8(uint32_t v) { return (uint32_t)(int32_t)(int8_t)(v & 0xFFu); }
 
-// LY poll loop: the six bytes at an address are LDH A,(44); CP d8; JR cc,-6
-// (jumping back to the LDH).  The record builder marks such an LDH (FL bit
-// 28, DW = d8 | cc << 8); while LY stays the same every pass through the
-// loop leaves the same A and F, so the step kernel may advance whole passes
-// at once (32 cycles, 3 instructions each) up to the next event.
-constexpr uint32_t kPollFlag = 1u << 28;
-__host__ __device__ constexpr bool poll_loop_at(const uint8_t* p) {
-  return p[0] == 0xF0u && p[1] == 0x44u && p[2] == 0xFEu &&
-         (p[4] == 0x20u || p[4] == 0x28u || p[4] == 0x30u || p[4] == 0x38u) && p[5] == 0xFAu;
+// LY poll loop: a load of LY into A (LDH A,(44), or LD A,(FF44)), CP d8,
+// and a conditional jump back to the load (JR cc with the displacement that
+// lands on it, or JP cc,a16).  The record builder marks such a load (FL bit
+// 28) with DW = d8 | cc << 8 | (pass cycles / 4) << 10 | JP << 14 | the JP
+// target << 16; while LY stays the same every pass leaves the same A and F,
+// so the step kernel may advance whole passes at once (3 instructions and
+// 32, 36 or 40 cycles each) up to the next event.  A JP's target is only
+// known as an address, so the kernel takes passes only when it is the pc of
+// the load.  `avail` is the number of bytes readable at p; the result is the
+// loop's length in bytes, 0 for no loop.
+__host__ __device__ constexpr uint32_t poll_loop_len(const uint8_t* p, uint32_t avail) {
+  uint32_t n = 0;  // bytes of the load
+  if (avail >= 2u && p[0] == 0xF0u && p[1] == 0x44u) n = 2;
+  else if (avail >= 3u && p[0] == 0xFAu && p[1] == 0x44u && p[2] == 0xFFu) n = 3;
+  if (n == 0u || avail < n + 4u || p[n] != 0xFEu) return 0;
+  const uint32_t j = p[n + 2];
+  if ((j == 0x20u || j == 0x28u || j == 0x30u || j == 0x38u) && p[n + 3] == ((0x100u - (n + 4u)) & 0xFFu))
+    return n + 4u;
+  // (a JP target at or above 0x8000 is never the load's pc: records exist
+  // only for ROM and the boot image, and bit 31 of DW marks a copy loop)
+  if ((j == 0xC2u || j == 0xCAu || j == 0xD2u || j == 0xDAu) && avail >= n + 5u && p[n + 4] < 0x80u)
+    return n + 5u;
+  return 0;
 }
+constexpr uint32_t kPollFlag = 1u << 28;
 __host__ __device__ constexpr Rec mark_poll_loop(Rec r, const uint8_t* p) {
+  const uint32_t n = p[0] == 0xF0u ? 2u : 3u;
+  const uint32_t j = p[n + 2];
+  const bool jp = (j & 0xC0u) == 0xC0u;
+  const uint32_t cc = ((j & 0x18u) >> 3);  // NZ Z NC C
+  const uint32_t cyc = (n == 2u ? 12u : 16u) + 8u + (jp ? 16u : 12u);
+  const uint32_t tgt = jp ? (uint32_t)p[n + 3] | ((uint32_t)p[n + 4] << 8) : 0u;
   r.w[10] |= kPollFlag;
-  r.w[15] = p[3] | (((uint32_t)(p[4] - 0x20u) >> 3) << 8);
+  r.w[15] = p[n + 1] | (cc << 8) | ((cyc / 4u) << 10) | ((jp ? 1u : 0u) << 14) | (tgt << 16);
   return r;
 }
 // The block-copy loop LD A,(HL+); LD (DE),A; INC DE; DEC BC; LD A,B; OR C

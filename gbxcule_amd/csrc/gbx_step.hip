@@ -993,9 +993,10 @@ struct Lane {
   __device__ bool ff_blocked() const {
     return (ime_delay != 0u) | ((ime != 0u) & ((ie & ifr & 0x1Fu) != 0u));
   }
-  // Whole passes of an LY poll loop (LDH A,(44); CP d8; JR cc,back; 32
-  // cycles) that can be taken in one step from the LDH that just read ly:
-  // 0 unless the jump back is taken.  The reference runs the loop one
+  // Whole passes of an LY poll loop (LDH A,(44) or LD A,(FF44); CP d8; JR cc
+  // or JP cc back to the load; 32, 36 or 40 cycles) that can be taken in one
+  // step from the load at pc that just read ly: 0 unless the jump back is
+  // taken (and, for a JP, lands on pc).  The reference runs the loop one
   // instruction at a time with the timer, PPU, interrupt check and frame
   // count after each.  The loop observes only the LY it reads, so the passes
   // run through scanline changes up to the first line whose value ends the
@@ -1004,14 +1005,23 @@ struct Lane {
   // serviced, or with the HBlank STAT source on the next mode boundary.  The
   // last pass ends at or before it.  A pass reads the line at its own start:
   // the one read now until the next change, then ly + 1, ly + 2, ...
-  __device__ int poll_passes(uint32_t dw, uint32_t ly_read, int cframe) const {
+  // Cycles of one pass of the poll loop whose record word is dw.
+  __device__ static uint32_t poll_pass_cycles(uint32_t dw) { return ((dw >> 10) & 0xFu) * 4u; }
+  // x / poll_pass_cycles(dw) for 0 <= x < 2^20 as one high multiply by the
+  // rounded-up reciprocal (exact for the 32-, 36- and 40-cycle passes there)
+  __device__ static uint32_t div_pass(uint32_t x, uint32_t dw) {
+    const uint32_t q = (dw >> 10) & 0xFu;  // 8, 9 or 10
+    const uint32_t m = q == 8u ? 0x08000000u : q == 9u ? 0x071C71C8u : 0x06666667u;
+    return __umulhi(x, m);
+  }
+  __device__ int poll_passes(uint32_t dw, uint32_t ly_read, int cframe, uint32_t pc) const {
     const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
     // cc: 0 NZ, 1 Z, 2 NC, 3 C
     const bool flag = (cc & 2u) ? ly_read < d8 : ly_read == d8;
-    const bool back = flag == ((cc & 1u) != 0u);
+    const bool back = (flag == ((cc & 1u) != 0u)) & (((dw >> 14) & 1u) == 0u || (dw >> 16) == pc);
     if ((!back) | ff_blocked()) return 0;
-    if (!(lcdc & 0x80u)) return ff_horizon(cframe, true, 0u) / 32;  // LY stays 0
-    int k = ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u) / 32;
+    if (!(lcdc & 0x80u)) return (int)div_pass((uint32_t)ff_horizon(cframe, true, 0u), dw);  // LY stays 0
+    int k = (int)div_pass((uint32_t)ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u), dw);
     // m = line changes ahead to the first line whose value ends the loop
     // (0: none does)
     const uint32_t nl = (uint32_t)kLinesPerFrame;
@@ -1025,7 +1035,7 @@ struct Lane {
     if (cc == 3u) m = d8 >= nl ? 0u : v1 >= d8 ? 1u : (d8 + nl - ly - 1u) % nl + 1u;
     if (m != 0u) {
       const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
-      k = min(k, (c + 31) / 32);
+      k = min(k, (int)div_pass((uint32_t)c + poll_pass_cycles(dw) - 1u, dw));
     }
     return k;
   }
@@ -1413,14 +1423,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
               ninstr += 7u * (uint32_t)k - 1u;
             }
           } else if (!dbg && (o.misc & 16u)) {
-            // LDH A,(44) just read LY into A; if CP d8 / JR cc takes the jump
-            // back, every pass until LY or anything else can change reads the
-            // same LY and leaves the same A and F: advance k whole passes (this
-            // LDH included) in one step.
-            const int k = L.poll_passes(rec.w[15], in.rd0, cframe);
+            // The load of an LY poll loop just read LY into A; if CP d8 and the
+            // jump take it back, every pass until LY or anything else can
+            // change reads the same LY and leaves the same A and F: advance k
+            // whole passes (this load included) in one step.
+            const int k = L.poll_passes(rec.w[15], in.rd0, cframe, pc);
             if (k > 0) {
-              // A and F as the last pass's LDH and CP leave them
-              const uint32_t off = L.scan + 32u * (uint32_t)(k - 1);
+              const uint32_t pcyc = Lane::poll_pass_cycles(rec.w[15]);
+              // A and F as the last pass's load and CP leave them
+              const uint32_t off = L.scan + pcyc * (uint32_t)(k - 1);
               const uint32_t ly = ((off < (uint32_t)kCyclesPerLine) | ((L.lcdc & 0x80u) == 0u))
                                       ? in.rd0
                                       : (L.ly + off / (uint32_t)kCyclesPerLine) % (uint32_t)kLinesPerFrame;
@@ -1429,8 +1440,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
                                  ((ly < d8) ? 0x10u : 0u);
               L.w1 = (L.w1 & 0xFFFF0000u) | (f << 8) | ly;
               npc = pc;
-              cycles = 32 * k;
-              rtc_pre = cycles - 12;
+              cycles = (int)pcyc * k;
+              rtc_pre = cycles - (((rec.w[15] >> 14) & 1u) ? 16 : 12);  // the JP or JR
               ninstr += 3u * (uint32_t)k - 1u;
             }
           }

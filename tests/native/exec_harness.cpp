@@ -74,13 +74,13 @@ void harness_exec(const uint32_t* in, uint32_t* out) {
   for (int k = 0; k < 12; ++k) out[k] = res[k];
 }
 
-// out: [is a poll-loop start, FL word, DW word] of the decoded and marked
-// record at p (6 bytes)
-void harness_poll(const uint8_t* p, uint32_t* out) {
+// out: [poll-loop length in bytes (0: none), FL word, DW word] of the decoded and marked
+// record at p (n bytes readable)
+void harness_poll(const uint8_t* p, uint32_t n, uint32_t* out) {
   gbx::Rec r = gbx::decode_insn(p[0], p[1], p[2]);
-  const bool poll = gbx::poll_loop_at(p);
-  if (poll) r = gbx::mark_poll_loop(r, p);
-  out[0] = poll ? 1u : 0u;
+  const uint32_t len = gbx::poll_loop_len(p, n);
+  if (len) r = gbx::mark_poll_loop(r, p);
+  out[0] = len;
   out[1] = r.w[10];
   out[2] = r.w[15];
 }

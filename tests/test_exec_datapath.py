@@ -44,7 +44,7 @@ def harness(tmp_path_factory):
     u32p = ctypes.POINTER(ctypes.c_uint32)
     lib.harness_decode.argtypes = [ctypes.c_uint32] * 3 + [u32p]
     lib.harness_exec.argtypes = [u32p, u32p]
-    lib.harness_poll.argtypes = [ctypes.c_char_p, u32p]
+    lib.harness_poll.argtypes = [ctypes.c_char_p, ctypes.c_uint32, u32p]
     lib.harness_copy.argtypes = [ctypes.c_char_p, u32p]
     return lib
 
@@ -202,23 +202,66 @@ def test_record_cycles_and_lengths_match_opcode_table(harness):
 
 
 def test_poll_loop_marking(harness):
-    """The record builder marks exactly LDH A,(44); CP d8; JR cc,-6 and
-    stores the compare constant and the jump condition."""
+    """The record builder marks exactly a load of LY into A (LDH A,(44) or
+    LD A,(FF44)), CP d8 and a conditional jump back (JR cc onto the load, or
+    JP cc,a16 below 0x8000, whose target the kernel checks against the pc),
+    and stores the compare constant, the condition, the pass cycles and the
+    JP target."""
     out = _arr(3)
-    for cc_op, cc in ((0x20, 0), (0x28, 1), (0x30, 2), (0x38, 3)):
-        harness.harness_poll(bytes([0xF0, 0x44, 0xFE, 0x90, cc_op, 0xFA]), out)
-        assert out[0] == 1 and out[1] & (1 << 28) and out[2] == 0x90 | (cc << 8)
-        # the LDH itself still decodes and executes as an LDH
-        assert (out[1] & ~(1 << 28)) & (0x7F << 24) == 0
+
+    def mark(code: bytes):
+        harness.harness_poll(code + bytes(8 - len(code)), len(code), out)
+        return int(out[0]), int(out[1]), int(out[2])
+
+    for load, ncyc in ((bytes([0xF0, 0x44]), 12), (bytes([0xFA, 0x44, 0xFF]), 16)):
+        n = len(load)
+        for cc in range(4):
+            jr = bytes([0x20 + 8 * cc, (0x100 - (n + 4)) & 0xFF])
+            ln, fl, dw = mark(load + bytes([0xFE, 0x90]) + jr)
+            assert ln == n + 4 and fl & (1 << 28)
+            assert dw == 0x90 | (cc << 8) | ((ncyc + 8 + 12) // 4 << 10)
+            # the load itself still decodes and executes as a load
+            assert (fl & ~(1 << 28)) & (0x7F << 24) == 0
+            jp = bytes([0xC2 + 8 * cc, 0x34, 0x12])
+            ln, fl, dw = mark(load + bytes([0xFE, 0x90]) + jp)
+            assert ln == n + 5 and fl & (1 << 28)
+            assert dw == 0x90 | (cc << 8) | ((ncyc + 8 + 16) // 4 << 10) | (1 << 14) | (0x1234 << 16)
     for bad in (
         [0xF0, 0x45, 0xFE, 0x90, 0x20, 0xFA],  # not LY
         [0xF0, 0x44, 0xE6, 0x90, 0x20, 0xFA],  # AND, not CP
         [0xF0, 0x44, 0xFE, 0x90, 0x18, 0xFA],  # unconditional JR
         [0xF0, 0x44, 0xFE, 0x90, 0x20, 0xFB],  # jumps elsewhere
-        [0xFA, 0x44, 0xFF, 0xFE, 0x90, 0x20],  # LD A,(a16) form
+        [0xFA, 0x44, 0xFF, 0xFE, 0x90, 0x20, 0xFA],  # LD A,(FF44) with the LDH's displacement
+        [0xFA, 0x45, 0xFF, 0xFE, 0x90, 0x20, 0xF9],  # LD A,(FF45)
+        [0xFA, 0x44, 0xFE, 0xFE, 0x90, 0x20, 0xF9],  # LD A,(FE44)
+        [0xF0, 0x44, 0xFE, 0x90, 0xC3, 0x50, 0x01],  # unconditional JP
+        [0xF0, 0x44, 0xFE, 0x90, 0xC2, 0x00, 0xC0],  # JP into RAM
+        [0xF0, 0x44, 0xFE, 0x90, 0xC4, 0x50, 0x01],  # CALL
+        [0xF0, 0x44, 0xFE],  # truncated
     ):
-        harness.harness_poll(bytes(bad), out)
-        assert out[0] == 0 and not out[1] & (1 << 28)
+        ln, fl, _ = mark(bytes(bad))
+        assert ln == 0 and not fl & (1 << 28), bad
+
+
+def test_poll_loops_in_carts_are_marked(harness):
+    """Every LY poll loop of the poll parity carts, in each of its forms, is
+    marked, so those tests run the batched passes; the two loads of the JP
+    pair are marked as well (their targets are only checked at run time)."""
+    from tests.test_gpu_poll import CASES, FORM_CASES, poll_cart
+
+    out = _arr(3)
+
+    def marked(rom: bytes) -> int:
+        return sum(1 for i in range(0x150, 0x8000 - 8)
+                   if (harness.harness_poll(rom[i : i + 8], 8, out), out[0])[1] != 0)  # fmt: skip
+
+    for case in CASES[:3]:
+        assert marked(poll_cart(*case)) == 4 + (1 if case[4] else 0)
+    forms = ("ld_jr", "ldh_jp", "ld_jp", "ldh_jr", "ld_jp")
+    for case in FORM_CASES:
+        seed, ime, ie, tac, lcd_off, stat, halt = case
+        rom = poll_cart(seed, ime, ie, tac, lcd_off, stat, halt, forms, True)
+        assert marked(rom) == 4 + (1 if lcd_off else 0) + 2
 
 
 def test_copy_loop_marking(harness):

@@ -1,7 +1,11 @@
-"""LY poll loops (LDH A,(44); CP d8; JR cc,back) against the oracle.
+"""LY poll loops (LDH A,(44) or LD A,(FF44); CP d8; JR cc or JP cc back to
+the load) against the oracle.
 
 The step kernel advances whole passes of such a loop in one step up to the
-next scanline, TIMA overflow, frame end or interrupt service.  These carts
+next scanline, TIMA overflow, frame end or interrupt service.  Besides the
+LDH/JR form the carts poll with LD A,(FF44) and with JP (passes of 36 and 40
+cycles), and with a pair of JP loops that jump to each other, which the
+kernel must run one instruction at a time.  These carts
 poll with every jump condition while timer, VBlank and STAT interrupts (LYC,
 HBlank and VBlank sources) fire with IME on or off, the LCD is switched off
 and on, and TIMA runs at every rate; state is compared in full after every
@@ -23,10 +27,29 @@ from .conftest import require_gpu
 pytestmark = pytest.mark.gpu
 
 
+FORMS = ("ldh_jr", "ld_jr", "ldh_jp", "ld_jp")
+
+
+def _poll(a: Asm, label: str, d8: int, cond: str, form: str) -> None:
+    """One LY poll loop in the given form: the load, CP d8, the jump back."""
+    a.label(label)
+    if form.startswith("ldh"):
+        a.ldh_a_a8(0x44)
+    else:
+        a.ld_a_a16(0xFF44)
+    a.alu_d8("CP", d8)
+    if form.endswith("jr"):
+        a.jr(label, cond)
+    else:
+        a.jp(label, cond)
+
+
 def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, stat: int = 0x40,
-              halt: bool = False) -> bytes:
+              halt: bool = False, forms: tuple[str, ...] = ("ldh_jr",), pair: bool = False) -> bytes:
     """A 32 KiB ROM-only cart whose main loop waits on LY four ways (and, with
-    ``halt``, in HALT until an interrupt request)."""
+    ``halt``, in HALT until an interrupt request); loop k is written in form
+    ``forms[k % len(forms)]``; with ``pair``, also two JP loops that jump to
+    each other."""
     rng = np.random.default_rng(seed)
     rom = bytearray(0x8000)
     h = Asm(origin=0x0068)
@@ -71,22 +94,22 @@ def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, sta
     a.ldh_a8_a(0x40)  # LCD on
     a.label("loop")
     lines = [int(x) for x in rng.integers(1, 153, 3)]
-    a.label("w1")  # until LY == 144
-    a.ldh_a_a8(0x44)
-    a.alu_d8("CP", 144)
-    a.jr("w1", "NZ")
-    a.label("w2")  # while LY == 144
-    a.ldh_a_a8(0x44)
-    a.alu_d8("CP", 144)
-    a.jr("w2", "Z")
-    a.label("w3")  # while LY < n
-    a.ldh_a_a8(0x44)
-    a.alu_d8("CP", lines[0])
-    a.jr("w3", "C")
-    a.label("w4")  # until LY < n (wraps through VBlank)
-    a.ldh_a_a8(0x44)
-    a.alu_d8("CP", lines[1])
-    a.jr("w4", "NC")
+    f = lambda k: forms[k % len(forms)]  # noqa: E731
+    _poll(a, "w1", 144, "NZ", f(0))  # until LY == 144
+    _poll(a, "w2", 144, "Z", f(1))  # while LY == 144
+    _poll(a, "w3", lines[0], "C", f(2))  # while LY < n
+    _poll(a, "w4", lines[1], "NC", f(3))  # until LY < n (wraps through VBlank)
+    if pair:  # until LY == n, alternating between two loads
+        a.label("pa")
+        a.ldh_a_a8(0x44)
+        a.alu_d8("CP", lines[2])
+        a.jp("pb", "NZ")
+        a.jp("pdone")
+        a.label("pb")
+        a.ld_a_a16(0xFF44)
+        a.alu_d8("CP", lines[2])
+        a.jp("pa", "NZ")
+        a.label("pdone")
     if halt:
         a.halt()
         a.nop()  # an IME=0 wake skips this byte
@@ -98,10 +121,7 @@ def poll_cart(seed: int, ime: bool, ie: int, tac: int, lcd_off_frames: bool, sta
         a.jr("loop", "NZ")
         a.ld_r_d8("A", 0x11)
         a.ldh_a8_a(0x40)  # LCD off: LY reads 0
-        a.label("w5")  # until LY == n: never, while the LCD is off
-        a.ldh_a_a8(0x44)
-        a.alu_d8("CP", lines[2])
-        a.jr("w5", "NZ")
+        _poll(a, "w5", lines[2], "NZ", f(4))  # until LY == n: never, while the LCD is off
     a.jp("loop")
     code = a.resolve()
     rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
@@ -136,13 +156,28 @@ HALT_CASES = [
 ]
 
 
-@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off,stat,halt",
-                         [c + (False,) for c in CASES] + [c + (True,) for c in HALT_CASES])  # fmt: skip
-def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat, halt):
+# The same waits written as LD A,(FF44) and JP loops (36- and 40-cycle
+# passes), mixed with the LDH/JR form, and the pair of JP loops that jump to
+# each other.
+FORM_CASES = [
+    (31, True, 0x07, 0x05, False, 0x40, False),
+    (32, False, 0x07, 0x07, True, 0x40, False),
+    (33, True, 0x02, 0x00, False, 0x08, False),
+    (34, True, 0x03, 0x05, False, 0x58, False),
+    (35, True, 0x06, 0x05, False, 0x10, True),
+    (36, True, 0x03, 0x04, True, 0x40, True),
+]
+
+
+@pytest.mark.parametrize("seed,ime,ie,tac,lcd_off,stat,halt,forms,pair",
+                         [c + (False, ("ldh_jr",), False) for c in CASES]
+                         + [c + (True, ("ldh_jr",), False) for c in HALT_CASES]
+                         + [c + (("ld_jr", "ldh_jp", "ld_jp", "ldh_jr", "ld_jp"), True) for c in FORM_CASES])  # fmt: skip
+def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat, halt, forms, pair):
     require_gpu()
     from gbxcule_amd.backend import HipVecBackend
 
-    rom = poll_cart(seed, ime, ie, tac, lcd_off, stat, halt)
+    rom = poll_cart(seed, ime, ie, tac, lcd_off, stat, halt, forms, pair)
     n, fs, steps = 64, 24, 4
     dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
                         stage="emulate_only", bootrom=bootstub)  # fmt: skip
