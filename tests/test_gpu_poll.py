@@ -5,7 +5,10 @@ The step kernel advances whole passes of such a loop in one step up to the
 next scanline, TIMA overflow, frame end or interrupt service.  Besides the
 LDH/JR form the carts poll with LD A,(FF44) and with JP (passes of 36 and 40
 cycles), and with a pair of JP loops that jump to each other, which the
-kernel must run one instruction at a time.  These carts
+kernel must run one instruction at a time.  STAT mode waits (LDH A,(41) or
+LD A,(FF41); AND m or BIT b,A; JR NZ or JR Z) run one instruction at a time
+and check that each read of STAT returns the mode of the exact cycle it
+falls on, between LY polls that are batched.  These carts
 poll with every jump condition while timer, VBlank and STAT interrupts (LYC,
 HBlank and VBlank sources) fire with IME on or off, the LCD is switched off
 and on, and TIMA runs at every rate; state is compared in full after every
@@ -197,6 +200,140 @@ def test_poll_loop_parity(bootstub, seed, ime, ie, tac, lcd_off, stat, halt, for
             assert int(mem[0, 0xDF02]) > 0  # timer interrupts were serviced
         if ime and ie & 2 and stat & 0x08:
             assert int(mem[0, 0xDF01]) > 0  # HBlank STAT interrupts were serviced
+        assert int(ref.field("trap_flag").sum()) == 0
+    finally:
+        dut.close()
+        ref.close()
+
+
+STAT_WAITS = (
+    # (load, op, operand, jump): AND m / BIT b,A, then JR NZ or JR Z back
+    ("ldh", "and", 3, "NZ"),  # until mode 0 (HBlank)
+    ("ldh", "and", 2, "NZ"),  # until mode 0 or 1
+    ("ld", "bit", 1, "NZ"),  # until mode 0 or 1, A keeps all of STAT
+    ("ldh", "and", 3, "Z"),  # while mode 0
+    ("ld", "and", 1, "NZ"),  # until mode 0 or 2
+    ("ldh", "bit", 0, "Z"),  # while mode 0 or 2
+    ("ld", "and", 2, "Z"),  # while mode 0 or 1 (through VBlank)
+)
+
+
+def _stat_wait(a: Asm, label: str, load: str, op: str, v: int, cond: str) -> None:
+    a.label(label)
+    if load == "ldh":
+        a.ldh_a_a8(0x41)
+    else:
+        a.ld_a_a16(0xFF41)
+    if op == "and":
+        a.alu_d8("AND", v)
+    else:
+        a.cb(0x47 | (v << 3))  # BIT v,A
+    a.jr(label, cond)
+
+
+def stat_cart(seed: int, ime: bool, ie: int, tac: int, stat: int, lcd_off_frames: bool) -> bytes:
+    """A 32 KiB ROM-only cart whose main loop runs every STAT mode wait of
+    STAT_WAITS, each after a joypad-dependent delay and between LY polls, with
+    timer, VBlank and STAT interrupts (handlers move LYC on)."""
+    rng = np.random.default_rng(seed)
+    rom = bytearray(0x8000)
+    h = Asm(origin=0x0068)
+    for name, counter in (("vbl", 0xDF00), ("stat", 0xDF01), ("timer", 0xDF02)):
+        h.label(name)
+        h.push("AF")
+        h.push("HL")
+        h.ld_rr_d16("HL", counter)
+        h.emit(0x34)  # INC (HL)
+        if name == "stat":
+            h.ldh_a_a8(0x45)
+            h.alu_d8("ADD", int(rng.integers(5, 40)))
+            h.alu_d8("CP", 154)
+            h.jr("lyc_ok", "C")
+            h.alu_d8("SUB", 154)
+            h.label("lyc_ok")
+            h.ldh_a8_a(0x45)
+        h.pop("HL")
+        h.pop("AF")
+        h.reti()
+    code = h.resolve()
+    rom[0x68 : 0x68 + len(code)] = code
+    _vectors(rom, {0x40: h.labels["vbl"], 0x48: h.labels["stat"], 0x50: h.labels["timer"]})
+
+    a = Asm(origin=PROGRAM_ORIGIN)
+    a.ld_rr_d16("SP", 0xDFF0)
+    for reg, val in ((0x06, int(rng.integers(0, 256))), (0x07, tac), (0x45, int(rng.integers(0, 154))),
+                     (0x41, stat), (0xFF, ie), (0x0F, 0)):  # fmt: skip
+        a.ld_r_d8("A", val)
+        a.ldh_a8_a(reg)
+    if ime:
+        a.ei()
+    a.ld_r_d8("A", 0x91)
+    a.ldh_a8_a(0x40)  # LCD on
+    a.label("loop")
+    for k, (load, op, v, cond) in enumerate(STAT_WAITS):
+        # a joypad-dependent delay, so that lanes reach the wait at
+        # different scanline positions
+        a.ld_r_d8("A", 0x10)
+        a.ldh_a8_a(0x00)
+        a.ldh_a_a8(0x00)
+        a.alu_d8("AND", 0x0F)
+        a.alu_d8("ADD", int(rng.integers(1, 30)))
+        a.ld_r_r("B", "A")
+        a.label(f"d{k}")
+        a.dec_r("B")
+        a.jr(f"d{k}", "NZ")
+        _stat_wait(a, f"s{k}", load, op, v, cond)
+        if k == 3:
+            _poll(a, "ly1", int(rng.integers(1, 153)), "NZ", "ldh_jr")
+    a.ld_a_a16(0xC000)
+    a.inc_r("A")
+    a.ld_a16_a(0xC000)
+    if lcd_off_frames:
+        a.alu_d8("AND", 0x03)
+        a.jp("loop", "NZ")
+        a.ld_r_d8("A", 0x11)
+        a.ldh_a8_a(0x40)  # LCD off: every mode reads 0
+        _stat_wait(a, "off1", "ldh", "and", 3, "NZ")  # exits at once
+        a.ld_r_d8("A", 0x91)
+        a.ldh_a8_a(0x40)  # LCD on again
+    a.jp("loop")
+    code = a.resolve()
+    rom[PROGRAM_ORIGIN : PROGRAM_ORIGIN + len(code)] = code
+    return finalize_rom(rom, "GBXAMD STAT", 0x00, 0x00, 0x00)
+
+
+STAT_CASES = [
+    # seed, IME, IE, TAC, STAT sources, LCD-off frames
+    (41, True, 0x07, 0x05, 0x40, False),
+    (42, False, 0x07, 0x06, 0x40, True),
+    (43, True, 0x02, 0x00, 0x08, False),  # HBlank STAT interrupts
+    (44, True, 0x03, 0x04, 0x50, True),
+    (45, True, 0x06, 0x07, 0x20, False),  # OAM source: never fires at a change
+    (46, False, 0x00, 0x00, 0x00, False),
+]
+
+
+@pytest.mark.parametrize("seed,ime,ie,tac,stat,lcd_off", STAT_CASES)
+def test_stat_wait_parity(bootstub, seed, ime, ie, tac, stat, lcd_off):
+    """STAT mode waits (every form of STAT_WAITS) against the oracle, full
+    state after every step."""
+    require_gpu()
+    from gbxcule_amd.backend import HipVecBackend
+
+    rom = stat_cart(seed, ime, ie, tac, stat, lcd_off)
+    n, fs, steps = 64, 12, 5
+    dut = HipVecBackend(rom, num_envs=n, frames_per_step=fs, release_after_frames=8,
+                        stage="emulate_only", bootrom=bootstub)  # fmt: skip
+    ref = RefMachine(n, rom, bootstub)
+    try:
+        dut.reset(seed=seed)
+        ref.step(None, 0, 0, "emulate_only")
+        for k in range(steps):
+            act = seeded_actions(seed, k, n)
+            dut.step(act)
+            ref.step(act, fs, 8, "emulate_only", threads=8)
+            assert_same_state(dut, ref, step=k, tag=f"stat{seed}")
+        assert int(ref.mem[:, 0xC000].min()) > 0  # the waits completed
         assert int(ref.field("trap_flag").sum()) == 0
     finally:
         dut.close()
