@@ -354,9 +354,11 @@ struct Lane {
   }
 
   // -- timer (cpu_step_builder.py:249-372) -------------------------------------
-  __device__ static uint32_t div_bit(uint32_t t) {
-    const uint32_t sl = t & 3u;
-    return sl == 0 ? 9u : sl == 1 ? 3u : sl == 2 ? 5u : 7u;
+  // TAC select 0..3 -> DIV bit 9, 3, 5, 7 (one nibble each)
+  __device__ static uint32_t div_bit(uint32_t t) { return (0x7539u >> ((t & 3u) << 2)) & 0xFu; }
+  // x mod 154 for x < 308 (a line number plus fewer than 154 changes)
+  __device__ static uint32_t wrap_line(uint32_t x) {
+    return x >= (uint32_t)kLinesPerFrame ? x - (uint32_t)kLinesPerFrame : x;
   }
   __device__ static uint32_t timer_in(uint32_t d, uint32_t t) {
     return (t & 4u) ? (d >> div_bit(t)) & 1u : 0u;
@@ -858,9 +860,7 @@ struct Lane {
         total -= kCyclesPerLine;
         const uint32_t pl = ly;
         wl += (uint32_t)((pl < (uint32_t)kScreenH) & ((lc & 0x20u) != 0u) & (pl >= wy));
-        uint32_t nl = ly + 1u;
-        if (nl >= (uint32_t)kLinesPerFrame) nl %= (uint32_t)kLinesPerFrame;
-        ly = nl;
+        ly = wrap_line(ly + 1u);
         wl = ly == 0u ? 0u : wl;
         lym = ly;
         // ppu_update_stat_irq with mode 0 or 1: bit0 mode 0, bit1 mode 1, bit3 LY == LYC
@@ -951,12 +951,14 @@ struct Lane {
   // line 144 (VBlank, and the STAT mode-1 source) or into line LYC (the STAT
   // LYC source).  The mode-2 source never fires at a change, and the HBlank
   // source is handled by the caller.
+  // (Selects throughout: these run in the rare blocks, where every branch
+  // costs the wavefront its exec-mask bookkeeping.)
   __device__ int line_horizon(uint32_t irq) const {
-    uint32_t n = 0xFFFFu;  // changes ahead, 1 = the next one
-    if (((irq & 1u) != 0u) | (((irq & 2u) != 0u) & ((stat_full & 0x10u) != 0u)))
-      n = (144u + 153u - ly) % (uint32_t)kLinesPerFrame + 1u;
-    if (((irq & 2u) != 0u) & ((stat_full & 0x40u) != 0u) & (lyc < (uint32_t)kLinesPerFrame))
-      n = min(n, (lyc + 153u - ly) % (uint32_t)kLinesPerFrame + 1u);
+    // changes ahead, 1 = the next one: into line 144 and into line LYC
+    const uint32_t n144 = wrap_line(144u + 153u - ly) + 1u;
+    const uint32_t nlyc = wrap_line(lyc + 153u - ly) + 1u;  // used only for lyc < 154
+    uint32_t n = ((irq & 1u) != 0u) | (((irq & 2u) != 0u) & ((stat_full & 0x10u) != 0u)) ? n144 : 0xFFFFu;
+    n = ((irq & 2u) != 0u) & ((stat_full & 0x40u) != 0u) & (lyc < (uint32_t)kLinesPerFrame) ? min(n, nlyc) : n;
     return n == 0xFFFFu ? kCyclesPerFrame : (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(n - 1u);
   }
   // Cycles from here to the nearest event that a batched step must not pass:
@@ -969,24 +971,15 @@ struct Lane {
   // start in mode 0 as the reference's last instruction of the line does, so
   // then every change and the mode boundaries count as well.
   __device__ int ff_horizon(int cframe, bool every_line, uint32_t irq) const {
-    int d = kCyclesPerFrame - cframe;
-    if (lcdc & 0x80u) {
-      if (every_line | ((stat_full & 0x08u) != 0u)) {
-        const bool hbl = (stat_full & 0x08u) != 0u && ly < (uint32_t)kScreenH;
-        const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
-        d = min(d, nb - (int)scan);
-      } else if (irq) {
-        d = min(d, line_horizon(irq));
-      }
-    }
-    if (pend) {
-      d = min(d, max((int)delay, 1));
-    } else if (tac & 4u) {
-      const int period = 1 << (div_bit(tac) + 1);
-      const int edge = period - (int)(div & (uint32_t)(period - 1));
-      d = min(d, edge + (int)(255u - tima) * period);
-    }
-    return d;
+    const int d = kCyclesPerFrame - cframe;
+    const bool hsrc = (stat_full & 0x08u) != 0u;
+    const bool hbl = hsrc & (ly < (uint32_t)kScreenH);
+    const int nb = !hbl ? kCyclesPerLine : scan < 80u ? 80 : scan < 250u ? 250 : kCyclesPerLine;
+    const int dl = (every_line | hsrc) ? nb - (int)scan : irq ? line_horizon(irq) : d;
+    const int period = 1 << (div_bit(tac) + 1);
+    const int edge = period - (int)(div & (uint32_t)(period - 1));
+    const int dt = pend ? max((int)delay, 1) : (tac & 4u) ? edge + (int)(255u - tima) * period : d;
+    return min(min(d, (lcdc & 0x80u) ? dl : d), dt);
   }
   // No pass may be batched while an interrupt would be serviced after the
   // current instruction or the EI delay is pending.
@@ -1019,25 +1012,24 @@ struct Lane {
     // cc: 0 NZ, 1 Z, 2 NC, 3 C
     const bool flag = (cc & 2u) ? ly_read < d8 : ly_read == d8;
     const bool back = (flag == ((cc & 1u) != 0u)) & (((dw >> 14) & 1u) == 0u || (dw >> 16) == pc);
-    if ((!back) | ff_blocked()) return 0;
-    if (!(lcdc & 0x80u)) return (int)div_pass((uint32_t)ff_horizon(cframe, true, 0u), dw);  // LY stays 0
-    int k = (int)div_pass((uint32_t)ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u), dw);
+    // (with the LCD off ff_horizon ignores the line arguments, and LY stays 0)
+    const int k = (int)div_pass((uint32_t)ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u), dw);
     // m = line changes ahead to the first line whose value ends the loop
     // (0: none does)
     const uint32_t nl = (uint32_t)kLinesPerFrame;
-    const uint32_t v1 = (ly + 1u) % nl;
+    const uint32_t v1 = wrap_line(ly + 1u);
+    const uint32_t dist = wrap_line(d8 + nl - ly - 1u) + 1u;  // used only for d8 < nl
     uint32_t m = 1u;  // Z: the first change (conservative: stopping early is exact)
-    if (cc == 0u) m = d8 < nl ? (d8 + nl - ly - 1u) % nl + 1u : 0u;   // NZ: until LY == d8
-    if (cc == 2u) m = d8 == 0u ? 0u : v1 < d8 ? 1u : nl - ly;         // NC: until LY < d8
+    m = cc == 0u ? (d8 < nl ? dist : 0u) : m;                       // NZ: until LY == d8
+    m = cc == 2u ? (d8 == 0u ? 0u : v1 < d8 ? 1u : nl - ly) : m;    // NC: until LY < d8
     // C: until LY >= d8.  From line 153 the changes run 0, 1, ..., d8, so d8 + 1
     // of them; (d8 + nl - ly - 1) % nl + 1 counts that and also the case
     // ly == d8 (a program that wrote FF44 reads a smaller LY): nl changes.
-    if (cc == 3u) m = d8 >= nl ? 0u : v1 >= d8 ? 1u : (d8 + nl - ly - 1u) % nl + 1u;
-    if (m != 0u) {
-      const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
-      k = min(k, (int)div_pass((uint32_t)c + poll_pass_cycles(dw) - 1u, dw));
-    }
-    return k;
+    m = cc == 3u ? (d8 >= nl ? 0u : v1 >= d8 ? 1u : dist) : m;
+    const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
+    const int km = (int)div_pass((uint32_t)c + poll_pass_cycles(dw) - 1u, dw);  // used only for m != 0
+    const int kk = ((lcdc & 0x80u) != 0u) & (m != 0u) ? min(k, km) : k;
+    return ((!back) | ff_blocked()) ? 0 : kk;
   }
   // End of the plain RAM window holding x (video RAM, work RAM), else 0.
   __device__ static uint32_t ram_window_end(uint32_t x) {
@@ -1434,7 +1426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
               const uint32_t off = L.scan + pcyc * (uint32_t)(k - 1);
               const uint32_t ly = ((off < (uint32_t)kCyclesPerLine) | ((L.lcdc & 0x80u) == 0u))
                                       ? in.rd0
-                                      : (L.ly + off / (uint32_t)kCyclesPerLine) % (uint32_t)kLinesPerFrame;
+                                      : Lane::wrap_line(L.ly + off / (uint32_t)kCyclesPerLine);
               const uint32_t d8 = rec.w[15] & 0xFFu;
               const uint32_t f = ((ly == d8) ? 0x80u : 0u) | 0x40u | (((ly & 15u) < (d8 & 15u)) ? 0x20u : 0u) |
                                  ((ly < d8) ? 0x10u : 0u);
