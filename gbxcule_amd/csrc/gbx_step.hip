@@ -957,8 +957,8 @@ struct Lane {
     // changes ahead, 1 = the next one: into line 144 and into line LYC
     const uint32_t n144 = wrap_line(144u + 153u - ly) + 1u;
     const uint32_t nlyc = wrap_line(lyc + 153u - ly) + 1u;  // used only for lyc < 154
-    uint32_t n = ((irq & 1u) != 0u) | (((irq & 2u) != 0u) & ((stat_full & 0x10u) != 0u)) ? n144 : 0xFFFFu;
-    n = ((irq & 2u) != 0u) & ((stat_full & 0x40u) != 0u) & (lyc < (uint32_t)kLinesPerFrame) ? min(n, nlyc) : n;
+    uint32_t n = (((irq & 1u) != 0u) | (((irq & 2u) != 0u) & ((stat_full & 0x10u) != 0u))) ? n144 : 0xFFFFu;
+    n = (((irq & 2u) != 0u) & ((stat_full & 0x40u) != 0u) & (lyc < (uint32_t)kLinesPerFrame)) ? min(n, nlyc) : n;
     return n == 0xFFFFu ? kCyclesPerFrame : (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(n - 1u);
   }
   // Cycles from here to the nearest event that a batched step must not pass:
@@ -1028,7 +1028,7 @@ struct Lane {
     m = cc == 3u ? (d8 >= nl ? 0u : v1 >= d8 ? 1u : dist) : m;
     const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
     const int km = (int)div_pass((uint32_t)c + poll_pass_cycles(dw) - 1u, dw);  // used only for m != 0
-    const int kk = ((lcdc & 0x80u) != 0u) & (m != 0u) ? min(k, km) : k;
+    const int kk = (((lcdc & 0x80u) != 0u) & (m != 0u)) ? min(k, km) : k;
     return ((!back) | ff_blocked()) ? 0 : kk;
   }
   // End of the plain RAM window holding x (video RAM, work RAM), else 0.
