@@ -1007,13 +1007,19 @@ struct Lane {
     const uint32_t m = q == 8u ? 0x08000000u : q == 9u ? 0x071C71C8u : 0x06666667u;
     return __umulhi(x, m);
   }
-  __device__ int poll_passes(uint32_t dw, uint32_t ly_read, int cframe, uint32_t pc) const {
+  // `ex` is set when the passes stop at the change into a line that ends the
+  // loop (not at an event) and the exit also fits before the event horizon:
+  // the next pass's load then reads that line, and its CP and the jump not
+  // taken can join the step (pass cycles - 4: the jump not taken is 4 cycles
+  // shorter), which saves the loop a second entry into this block.
+  __device__ int poll_passes(uint32_t dw, uint32_t ly_read, int cframe, uint32_t pc, bool& ex) const {
     const uint32_t d8 = dw & 0xFFu, cc = (dw >> 8) & 3u;
     // cc: 0 NZ, 1 Z, 2 NC, 3 C
     const bool flag = (cc & 2u) ? ly_read < d8 : ly_read == d8;
     const bool back = (flag == ((cc & 1u) != 0u)) & (((dw >> 14) & 1u) == 0u || (dw >> 16) == pc);
     // (with the LCD off ff_horizon ignores the line arguments, and LY stays 0)
-    const int k = (int)div_pass((uint32_t)ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u), dw);
+    const int h = ff_horizon(cframe, false, ime != 0u ? ie & 0x03u : 0u);
+    const int k = (int)div_pass((uint32_t)h, dw);
     // m = line changes ahead to the first line whose value ends the loop
     // (0: none does)
     const uint32_t nl = (uint32_t)kLinesPerFrame;
@@ -1028,8 +1034,12 @@ struct Lane {
     m = cc == 3u ? (d8 >= nl ? 0u : v1 >= d8 ? 1u : dist) : m;
     const int c = (kCyclesPerLine - (int)scan) + kCyclesPerLine * (int)(m - 1u);
     const int km = (int)div_pass((uint32_t)c + poll_pass_cycles(dw) - 1u, dw);  // used only for m != 0
-    const int kk = (((lcdc & 0x80u) != 0u) & (m != 0u)) ? min(k, km) : k;
-    return ((!back) | ff_blocked()) ? 0 : kk;
+    const bool ends = ((lcdc & 0x80u) != 0u) & (m != 0u);
+    const int kk = ends ? min(k, km) : k;
+    const int pcyc = (int)poll_pass_cycles(dw);
+    const bool none = (!back) | ff_blocked();
+    ex = (!none) & ends & (km <= k) & (km * pcyc + pcyc - 4 <= h);
+    return none ? 0 : kk;
   }
   // End of the plain RAM window holding x (video RAM, work RAM), else 0.
   __device__ static uint32_t ram_window_end(uint32_t x) {
@@ -1419,11 +1429,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
             // jump take it back, every pass until LY or anything else can
             // change reads the same LY and leaves the same A and F: advance k
             // whole passes (this load included) in one step.
-            const int k = L.poll_passes(rec.w[15], in.rd0, cframe, pc);
+            bool ex = false;
+            const int k = L.poll_passes(rec.w[15], in.rd0, cframe, pc, ex);
             if (k > 0) {
               const uint32_t pcyc = Lane::poll_pass_cycles(rec.w[15]);
-              // A and F as the last pass's load and CP leave them
-              const uint32_t off = L.scan + pcyc * (uint32_t)(k - 1);
+              const uint32_t jp = (rec.w[15] >> 14) & 1u;
+              // A and F as the last pass's load and CP leave them, or with the
+              // exit those of the load after the k passes
+              const uint32_t off = L.scan + pcyc * (uint32_t)(k - (ex ? 0 : 1));
               const uint32_t ly = ((off < (uint32_t)kCyclesPerLine) | ((L.lcdc & 0x80u) == 0u))
                                       ? in.rd0
                                       : Lane::wrap_line(L.ly + off / (uint32_t)kCyclesPerLine);
@@ -1431,10 +1444,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
               const uint32_t f = ((ly == d8) ? 0x80u : 0u) | 0x40u | (((ly & 15u) < (d8 & 15u)) ? 0x20u : 0u) |
                                  ((ly < d8) ? 0x10u : 0u);
               L.w1 = (L.w1 & 0xFFFF0000u) | (f << 8) | ly;
-              npc = pc;
-              cycles = (int)pcyc * k;
-              rtc_pre = cycles - (((rec.w[15] >> 14) & 1u) ? 16 : 12);  // the JP or JR
-              ninstr += 3u * (uint32_t)k - 1u;
+              // the load (LDH 2 bytes, LD A,(a16) 3), CP d8 and the jump (JR 2, JP 3)
+              const uint32_t len = (op == 0xFAu ? 3u : 2u) + 2u + 2u + jp;
+              npc = ex ? (pc + len) & 0xFFFFu : pc;
+              cycles = (int)pcyc * k + (ex ? (int)pcyc - 4 : 0);
+              // the cycles before the last instruction, the jump: taken (JP 16,
+              // JR 12) or, after the exit, not taken (JP 12, JR 8)
+              rtc_pre = cycles - (jp ? 16 : 12) + (ex ? 4 : 0);
+              ninstr += 3u * (uint32_t)k - 1u + (ex ? 3u : 0u);
             }
           }
         }
