@@ -70,3 +70,46 @@ def test_snapshot_render_random_scenes(carts, bootstub, n, seed):
     finally:
         dut.close()
         ref.close()
+
+
+# LCDC per group of 8 envs (the envs a render workgroup takes together):
+# BG through 9800 or 9C00 with 8000 tiles, BG and window on different maps,
+# the signed 9000 tile data, BG off (sprites only), and groups mixing two
+# settings.
+LCDC_GROUPS = [
+    (0x91,), (0x99,), (0xF3,), (0xB1,), (0xE3,), (0x83,), (0x90,), (0x02,),
+    (0x91, 0x99), (0x93, 0x83), (0xF1, 0x90),
+]
+
+
+@pytest.mark.parametrize("n,seed", [(256, 11), (8192, 12)])
+def test_snapshot_render_group_lcdc(carts, bootstub, n, seed):
+    """Every group of 8 envs shares one LCDC pattern (random scenes give a
+    group eight independent ones); VRAM everywhere is random."""
+    require_gpu()
+    from gbxcule_amd.backend import HipVecBackend
+
+    rom = carts["c1"]
+    dut = HipVecBackend(rom, num_envs=n, frames_per_step=1, release_after_frames=1,
+                        render_pixels=True, render_pixels_packed=False, render_on_step=False,
+                        bootrom=bootstub)  # fmt: skip
+    ref = RefMachine(n, rom, bootstub)
+    rng = np.random.default_rng(seed)
+    try:
+        dut.reset(seed=0)
+        ref.step(None, 0, 0, "full_step")
+        for e in range(n):
+            scene = _scene(rng)
+            pat = LCDC_GROUPS[(e // 8) % len(LCDC_GROUPS)]
+            io = bytearray(scene[0xFF40])
+            io[0] = pat[e % len(pat)]
+            scene[0xFF40] = bytes(io)
+            for addr, data in scene.items():
+                dut.write_memory(e, addr, data)
+                ref.mem[e, addr : addr + len(data)] = np.frombuffer(data, np.uint8)
+        dut.render_pixels_snapshot()
+        ref.render(packed=False, threads=8)
+        np.testing.assert_array_equal(dut.pixels_torch().cpu().numpy(), ref.pix)
+    finally:
+        dut.close()
+        ref.close()
