@@ -215,7 +215,13 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       fetch(nblk_next, npart, K0{}, KH{});
     }
     const uint32_t env = tid & (uint32_t)(kImgEnvs - 1);
-    const uint32_t oy = tid / (uint32_t)kImgEnvs;
+    // Wavefront w renders the 8 output rows of row block perm[w].  The 9
+    // wavefronts sit on the 4 SIMDs as w mod 4, so SIMD 0 carries three of
+    // them: it gets the three top blocks, and the bottom blocks, where a
+    // status-bar window adds a second layer, go to SIMDs with two.
+    constexpr uint64_t kRowBlock = 0x267815430ull;  // perm = 0 3 4 5 1 8 7 6 2
+    const uint32_t rblk = (uint32_t)(kRowBlock >> (4u * (tid >> 6))) & 0xFu;
+    const uint32_t oy = rblk * 8u + ((tid >> 3) & 7u);
     const uint32_t y = oy * 2u;
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&obj[g][tid][0]) = make_uint2(0u, 0u);
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       for (uint32_t d = 4u * lane; d < 64u * nw; d += 256u) {
         const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
         if (env0 + e < (uint32_t)s.n)
-          *reinterpret_cast<uint4*>(out + base + (size_t)(env0 + e) * env_bytes + wave * 32u * nw + 4u * w2) =
+          *reinterpret_cast<uint4*>(out + base + (size_t)(env0 + e) * env_bytes + rblk * 32u * nw + 4u * w2) =
               *reinterpret_cast<const uint4*>(wst + d);
       }
     } else {
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
         const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
         if (env0 + e < (uint32_t)s.n) {
           const uint32_t wd = wst[d];
-          uint8_t* p = out + base + (size_t)(env0 + e) * env_bytes + wave * 32u * nw + 4u * w2;
+          uint8_t* p = out + base + (size_t)(env0 + e) * env_bytes + rblk * 32u * nw + 4u * w2;
           if (aligned) {
             *reinterpret_cast<uint32_t*>(p) = wd;
           } else {
