@@ -1368,8 +1368,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
             p1 = L.bus_ptr(x1);
           v1 = ld_global(p1);
         }
-        in.rd0 = nr != 0u ? L.bus_fix(x0, v0) : 0u;
-        in.rd1 = nr > 1u ? L.bus_fix(x1, v1) : in.rd0;
+        // DIV, TIMA, STAT and LY (FF04 FF05 FF40 FF41 FF44 FF45, bus_fix's
+        // test) for both bytes behind one wave-uniform test, the bytes
+        // taken by selects
+        const bool h0 = (nr != 0u) & ((x0 & 0xFFBAu) == 0xFF00u) & (x0 > 0xFF01u);
+        const bool h1 = (nr > 1u) & ((x1 & 0xFFBAu) == 0xFF00u) & (x1 > 0xFF01u);
+        uint32_t r0 = v0, r1 = v1;
+        if (__builtin_expect(__ballot(h0 | h1) != 0u, 0)) {
+          r0 = h0 ? L.read_ppu(x0, v0) : v0;
+          r1 = h1 ? L.read_ppu(x1, v1) : v1;
+        }
+        in.rd0 = nr != 0u ? r0 : 0u;
+        in.rd1 = nr > 1u ? r1 : in.rd0;
       }
 
       // ---- execute (gbx_exec.h) -------------------------------------------------
