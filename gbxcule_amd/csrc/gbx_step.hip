@@ -1438,7 +1438,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kMbc != MB
             // The load of an LY poll loop just read LY into A; if CP d8 and the
             // jump take it back, every pass until LY or anything else can
             // change reads the same LY and leaves the same A and F: advance k
-            // whole passes (this load included) in one step.
+            // whole passes (this load included) in one step, and when they
+            // end at the change into the line that ends the loop (ex), the
+            // exit too: the next load reads that line, CP sets F and the jump
+            // falls through.
             bool ex = false;
             const int k = L.poll_passes(rec.w[15], in.rd0, cframe, pc, ex);
             if (k > 0) {
