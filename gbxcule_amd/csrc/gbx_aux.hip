@@ -78,6 +78,23 @@ constexpr int kTileSlots = 21;     // tile columns one 80-sample row can touch
 constexpr int kGroups = kDsW / 4;  // 4-sample groups per row (one output word unpacked)
 static_assert(kImgEnvs == 8, "image rows are 8 bytes");
 
+// The image rows that four envs' renders read, from their LCDC bytes x, as
+// a mask of 1 KiB video RAM chunks (bit c: 8000 + 400h * c .. + 3FFh) and
+// bit 8 for OAM and the registers: sprite tiles 8000-8FFF with sprites on
+// (bit 1); with the BG on (bit 0) the BG and window tile block (8000-8FFF
+// with bit 4 set, else 8800-97FF) and the maps the background (bit 3) and
+// the window (bits 5 and 6) select.
+__device__ __forceinline__ uint32_t image_chunks(uint32_t x) {
+  constexpr uint32_t kB = 0x01010101u;
+  const uint32_t bg = x & kB, w = bg & (x >> 5);
+  const uint32_t lo_tiles = ((x >> 1) | (bg & (x >> 4))) & kB;     // 8000-8FFF
+  const uint32_t hi_tiles = bg & ~(x >> 4) & kB;                  // 8800-97FF
+  const uint32_t map1 = ((bg & (x >> 3)) | (w & (x >> 6))) & kB;  // 9C00-9FFF
+  const uint32_t map0 = ((bg & ~(x >> 3)) | (w & ~(x >> 6))) & kB;
+  return (lo_tiles ? 0x0Fu : 0u) | (hi_tiles ? 0x3Cu : 0u) | (map0 ? 0x40u : 0u) | (map1 ? 0x80u : 0u) |
+         0x100u;
+}
+
 struct Img {
   const uint8_t* p;  // the workgroup's image
   uint32_t env;      // 0..7
@@ -125,8 +142,12 @@ __device__ __forceinline__ void layer_tiles(const Src& r, uint32_t lcdc, uint32_
 }
 
 // One workgroup per 8 envs: it copies their image rows into LDS (every
-// thread issues all its loads before its LDS stores), then renders one
-// (env, output row) per thread.  The 8 workgroups of a 64-env block are
+// thread issues all its loads before its LDS stores; the 1 KiB video RAM
+// chunks that none of the 8 envs' LCDC lets the render read are skipped),
+// then renders one (env, output row) per thread.  Each image load brings a
+// 128-byte line for 16 useful bytes, so the CU's supply of L1 misses, not
+// HBM, bounds the copy: fewer lines and loads spread over the group are
+// what speed it up.  The 8 workgroups of a 64-env block are
 // dealt to one XCD (the hardware deals workgroup i to XCD i mod 8), so each
 // 64-byte line comes from HBM about once and its other reads hit that XCD's
 // L2.  Per row, the sprites (the first 10 OAM entries covering the line,
@@ -172,29 +193,57 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
     }
   };
   // image rows k0 <= k < k1 of each thread for a group, the loads issued
-  // together
+  // together, those in chunks outside `need` (image_chunks) skipped: the
+  // LDS rows they would fill get zeros no render of the group reads.  A
+  // wavefront's 64 rows of one load are 64-aligned, so they lie in one
+  // chunk and the test is wavefront-uniform.  The loads address the 64-env
+  // block as a raw buffer, a skipped one at an offset past its end, which
+  // returns zeros without a memory request (a branch around the load would
+  // make the compiler drain every outstanding load before the next one).
   uint2 v[kImgLoads];
-  auto fetch = [&](uint32_t blk, uint32_t part, auto k0, auto k1) {
-    const uint8_t* src = s.mem + ((size_t)blk << 22) + part * (uint32_t)kImgEnvs;
+  const uint32_t wrow = __builtin_amdgcn_readfirstlane(tid0 >> 6) * 64u;
+  auto fetch = [&](uint32_t blk, uint32_t part, uint32_t need, auto k0, auto k1) {
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        s.mem + ((size_t)blk << 22), 0, 1 << 22, 0x00020000);  // untyped raw buffer
     // (recomputed per call: kept across the loop, the 15 offsets would hold
     // registers the render needs)
     uint32_t t = tid0;
     asm volatile("" : "+v"(t));
+    __builtin_assume(t < (uint32_t)kImgThreads);  // only the last load reaches past video RAM
 #pragma unroll
     for (int k = decltype(k0)::value; k < decltype(k1)::value; ++k) {
       const uint32_t i = min(t + (uint32_t)k * kImgThreads, kImgRows - 1u);
       const uint32_t a = i < kImgVram ? 0x8000u + i
                          : i < kImgVram + kImgOam ? 0xFE00u + (i - kImgVram)
                                                   : 0xFF40u + (i - kImgVram - kImgOam);
-      v[k] = *reinterpret_cast<const uint2*>(src + ((size_t)a << kEnvBlockShift));
+      const bool want = (need >> ((wrow + (uint32_t)k * kImgThreads) >> 10)) & 1u;
+      const auto w = __builtin_amdgcn_raw_buffer_load_b64(rb, (int)(want ? a << kEnvBlockShift : 0x80000000u),
+                                                          (int)(part * (uint32_t)kImgEnvs), 0);
+      v[k] = make_uint2(w[0], w[1]);
     }
+  };
+  // a group's 8 LCDC bytes (one broadcast load), for its chunk mask
+  auto lcdc_row = [&](uint32_t blk, uint32_t part) {
+    return *reinterpret_cast<const uint2*>(s.mem + ((size_t)blk << 22) + part * (uint32_t)kImgEnvs +
+                                           ((size_t)0xFF40u << kEnvBlockShift));
+  };
+  auto chunks_of = [](uint2 x) {
+    return image_chunks(__builtin_amdgcn_readfirstlane(x.x)) | image_chunks(__builtin_amdgcn_readfirstlane(x.y));
   };
   uint32_t blk, part;
   using K0 = std::integral_constant<int, 0>;
-  using KH = std::integral_constant<int, kImgLoads / 2 + 1>;
+  using K3 = std::integral_constant<int, 3>;
+  using K8 = std::integral_constant<int, 8>;
   using KN = std::integral_constant<int, kImgLoads>;
   group(0u, blk, part);
-  fetch(blk, part, K0{}, KN{});
+  fetch(blk, part, 0x1FFu, K0{}, KN{});
+  // the LCDC bytes of group it + 1 load one group ahead of its rows
+  uint2 lc_next = make_uint2(0u, 0u);
+  if (rounds > 1u) {
+    uint32_t b1, p1;
+    group(1u, b1, p1);
+    lc_next = lcdc_row(b1, p1);
+  }
 #pragma unroll 1
   for (uint32_t it = 0; it < rounds; ++it) {
     // (derived per round: kept across the loop, the addresses that follow
@@ -206,13 +255,22 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       const uint32_t i = tid + (uint32_t)k * kImgThreads;
       if (i < kImgRows) *reinterpret_cast<uint2*>(img + (size_t)i * kImgEnvs) = v[k];
     }
-    // the next group's rows load while this one renders: the first half
-    // now, the rest once the tile rows below no longer hold registers
-    uint32_t nblk_next = 0, npart = 0;
+    // The next group's rows load while this one renders, in three parts:
+    // loads 0-2 once the coverage is marked, 3-7 after the sprites, 8-14
+    // after the BG and window layers (their tile rows then no longer hold
+    // registers).  Issued at once, the loads of the 9 wavefronts queue in
+    // the CU's memory pipeline and hold each wavefront at the issue of its
+    // last one; spread over the group, they stream beside the render.
+    uint32_t nblk_next = 0, npart = 0, need = 0;
     const bool more = it + 1u < rounds;
     if (more) {
       group(it + 1u, nblk_next, npart);
-      fetch(nblk_next, npart, K0{}, KH{});
+      need = chunks_of(lc_next);
+      if (it + 2u < rounds) {
+        uint32_t b2, p2;
+        group(it + 2u, b2, p2);
+        lc_next = lcdc_row(b2, p2);
+      }
     }
     const uint32_t env = tid & (uint32_t)(kImgEnvs - 1);
     // Wavefront w renders the 8 output rows of row block perm[w].  The 9
@@ -246,6 +304,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       }
     }
     __syncthreads();
+    if (more) fetch(nblk_next, npart, need, K0{}, K3{});
     const uint32_t lcdc = r.reg(0xFF40);
     const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
     const uint32_t scy = r.reg(0xFF42), scx = r.reg(0xFF43);
@@ -318,6 +377,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       }
     }
 
+    if (more) fetch(nblk_next, npart, need, K3{}, K8{});
     const uint32_t bg_on = (lcdc & 0x01u) ? ~0u : 0u;
     const bool win = (lcdc & 0x20u) && y >= wy;
     const int wx7 = (int)wx - 7;
@@ -341,7 +401,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
         layer_tiles(r, lcdc, sw, pyw, id, cw);
       }
     }
-    if (more) fetch(nblk_next, npart, KH{}, KN{});
+    if (more) fetch(nblk_next, npart, need, K8{}, KN{});
     const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
     // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
     const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
