@@ -435,22 +435,25 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       if (!packed) word[g] = shade;
     }
     // The stage: per wavefront (8 output rows of the 8 envs) its words in
-    // output order, env by env, row by row.
-    __syncthreads();
+    // output order, env by env, row by row, in the wavefront's own sprite
+    // line slots: stage word d in the 128 words of obj[d >> 7][64 wave ..
+    // 64 wave + 63].  No other wavefront touches them, so staging needs no
+    // barrier, and a wavefront done early stores its rows while the others
+    // still render.
     const uint32_t wave = tid >> 6, lane = tid & 63u, r8 = oy & 7u;
-    uint32_t* stage = reinterpret_cast<uint32_t*>(&obj[0][0][0]);
+    uint32_t* const slots = reinterpret_cast<uint32_t*>(&obj[0][0][0]) + wave * 128u;
+    auto stage = [&](uint32_t d) { return slots + (d >> 7) * (2u * (uint32_t)kImgThreads) + (d & 127u); };
     constexpr uint32_t nw = packed ? (uint32_t)kDsWB / 4u : (uint32_t)kGroups;  // words per row
-    uint32_t* mine = stage + wave * 64u * nw + (env * 8u + r8) * nw;
+    static_assert(64u * nw <= 128u * (uint32_t)kGroups, "a wavefront's stage fits its slots");
+    const uint32_t mine = (env * 8u + r8) * nw;
 #pragma unroll
     for (int g = 0; g < kGroups; ++g)
-      if ((uint32_t)g < nw) mine[g] = word[g];
-    __syncthreads();
+      if ((uint32_t)g < nw) *stage(mine + (uint32_t)g) = word[g];
     constexpr size_t env_bytes = (size_t)nw * 4u * kDsH;
     const uint32_t env0 = blk * (uint32_t)kEnvBlock + part * (uint32_t)kImgEnvs;
     // The wavefront's words in output order: env e's 8 rows are 8 * nw
     // consecutive words of its output, from byte wave * 32 * nw on.
     const uintptr_t ob = (uintptr_t)(out + base);
-    const uint32_t* wst = stage + wave * 64u * nw;
     if ((ob & 15u) == 0u) {
       // 16 bytes per lane (an env's words are a multiple of 4)
 #pragma unroll
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
         const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
         if (env0 + e < (uint32_t)s.n)
           *reinterpret_cast<uint4*>(out + base + (size_t)(env0 + e) * env_bytes + rblk * 32u * nw + 4u * w2) =
-              *reinterpret_cast<const uint4*>(wst + d);
+              *reinterpret_cast<const uint4*>(stage(d));
       }
     } else {
       const bool aligned = (ob & 3u) == 0u;
@@ -466,7 +469,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       for (uint32_t d = lane; d < 64u * nw; d += 64u) {
         const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
         if (env0 + e < (uint32_t)s.n) {
-          const uint32_t wd = wst[d];
+          const uint32_t wd = *stage(d);
           uint8_t* p = out + base + (size_t)(env0 + e) * env_bytes + rblk * 32u * nw + 4u * w2;
           if (aligned) {
             *reinterpret_cast<uint32_t*>(p) = wd;
