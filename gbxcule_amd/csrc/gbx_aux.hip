@@ -99,6 +99,8 @@ struct Img {
   const uint8_t* p;  // the workgroup's image
   uint32_t env;      // 0..7
   __device__ uint32_t M(uint32_t addr) const { return p[((addr - 0x8000u) << 3) | env]; }  // video RAM
+  __device__ uint32_t off(uint32_t addr) const { return ((addr - 0x8000u) << 3) | env; }  // M's byte
+  __device__ uint32_t at(uint32_t o) const { return p[o]; }
   __device__ uint32_t oam(uint32_t i) const { return p[((kImgVram + i) << 3) | env]; }
   __device__ uint32_t reg(uint32_t addr) const { return p[((kImgVram + kImgOam + addr - 0xFF40u) << 3) | env]; }
 };
@@ -123,21 +125,27 @@ __device__ __forceinline__ uint32_t spread_tile(uint32_t t, uint32_t p) {
 // Sample ox is then byte ox + ((s & 7) >> 1) of the byte stream c[0], c[1], ...
 // The 21 map reads of a layer are independent (layer_ids), then its 42
 // tile-data reads are (layer_tiles).
-template <class Src>
-__device__ __forceinline__ void layer_ids(const Src& r, uint32_t map, uint32_t s, uint32_t py,
+__device__ __forceinline__ void layer_ids(const Img& r, uint32_t map, uint32_t s, uint32_t py,
                                           uint32_t (&id)[kTileSlots]) {
-  const uint32_t mrow = map + (py >> 3) * 32u;
+  // map row (py >> 3): its 32 ids are 32 address rows of 8 bytes from an
+  // offset whose low 8 bits are the env, column (c + j) & 31 at 8 times that
+  const uint32_t row = r.off(map + (py >> 3) * 32u), c8 = s & 0xF8u;
 #pragma unroll
-  for (int j = 0; j < kTileSlots; ++j) id[j] = r.M(mrow + (((s >> 3) + (uint32_t)j) & 31u));
+  for (int j = 0; j < kTileSlots; ++j) id[j] = r.at(((c8 + 8u * (uint32_t)j) & 0xF8u) | row);
 }
-template <class Src>
-__device__ __forceinline__ void layer_tiles(const Src& r, uint32_t lcdc, uint32_t s, uint32_t py,
+// Tile id's row in the block LCDC bit 4 selects: 8000 + 16 id, or with
+// signed ids 9000 + 16 (int8)id = 8800 + 16 (id ^ 80h); in the image, the
+// row's low byte at offset((8000 or 8800) + 2 * row) + ((id ^ x) << 7), its
+// high byte 8 further (one address row).
+__device__ __forceinline__ void layer_tiles(const Img& r, uint32_t lcdc, uint32_t s, uint32_t py,
                                             const uint32_t (&id)[kTileSlots], uint32_t (&c)[kTileSlots]) {
-  const uint32_t row2 = (py & 7u) * 2u;
+  const bool unsigned_ids = (lcdc & 0x10u) != 0u;
+  const uint32_t x = unsigned_ids ? 0u : 0x80u;
+  const uint32_t b = r.off((unsigned_ids ? 0x8000u : 0x8800u) + (py & 7u) * 2u);
 #pragma unroll
   for (int j = 0; j < kTileSlots; ++j) {
-    const uint32_t ta = bg_tile_addr(lcdc, id[j]) + row2;
-    c[j] = spread_tile(r.M(ta) | (r.M(ta + 1u) << 8), s & 1u);
+    const uint32_t o = b + ((id[j] ^ x) << 7);
+    c[j] = spread_tile(r.at(o) | (r.at(o + 8u) << 8), s & 1u);
   }
 }
 
@@ -165,14 +173,20 @@ __device__ __forceinline__ void layer_tiles(const Src& r, uint32_t lcdc, uint32_
 template <bool packed>
 __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t* out, int64_t base,
                                                              uint32_t rounds) {
-  __shared__ __align__(16) uint8_t img[kImgRows * kImgEnvs];
-  // OAM entries covering each (env, output row): bit k = entry k
-  __shared__ uint64_t cover[kDsH][kImgEnvs];
+  // One LDS block, the image first: at LDS address 0 its data-dependent
+  // reads need no base added to their offsets.
+  constexpr size_t kImgBytes = (size_t)kImgRows * kImgEnvs;
+  constexpr size_t kObjBytes = (size_t)kGroups * kImgThreads * 4 * sizeof(uint16_t);
+  static_assert(kImgBytes % 16 == 0, "the sprite line buffer stays 16-byte aligned");
+  __shared__ uint4 lds[(kImgBytes + kObjBytes + (size_t)kDsH * kImgEnvs * sizeof(uint64_t)) / 16];
+  uint8_t* const img = reinterpret_cast<uint8_t*>(lds);
   // sprite line buffer, 4 samples per (group, thread): 0 = no sprite pixel,
   // else bits [0:1] its shade (palette applied), [2] behind non-zero BG, [3]
   // set, [8:15] the sprite's OAM x (its left edge + 8); reused as the
   // output stage
-  __shared__ __align__(16) uint16_t obj[kGroups][kImgThreads][4];
+  auto obj = reinterpret_cast<uint16_t(*)[kImgThreads][4]>(img + kImgBytes);
+  // OAM entries covering each (env, output row): bit k = entry k
+  auto cover = reinterpret_cast<uint64_t(*)[kImgEnvs]>(img + kImgBytes + kObjBytes);
   const uint32_t tid0 = threadIdx.x;
   const uint32_t nblk = (uint32_t)s.npad >> kEnvBlockShift;
   // Group `it` of this workgroup: (64-env block, eighth).  With rounds > 1
@@ -382,9 +396,16 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
     const bool win = (lcdc & 0x20u) && y >= wy;
     const int wx7 = (int)wx - 7;
     const uint32_t sw = (7u - wx) & 0xFFu;  // window: px = (x - (WX - 7)) & 0xFF
+    // A layer not drawn leaves its colours unset (defined by an empty asm,
+    // no instruction): the shading masks them out of every sample (the BG
+    // off clears all; a window covering the row takes every sample from
+    // the window, one starting past the row none).
     uint32_t cb[kTileSlots], cw[kTileSlots];
 #pragma unroll
-    for (int j = 0; j < kTileSlots; ++j) cb[j] = cw[j] = 0;
+    for (int j = 0; j < kTileSlots; ++j) {
+      asm volatile("" : "=v"(cb[j]));
+      asm volatile("" : "=v"(cw[j]));
+    }
     if (bg_on) {
       // the background unless the window covers the whole row
       const bool do_bg = !(win && wx7 <= 0), do_win = win && wx7 < 2 * kDsW - 1;
