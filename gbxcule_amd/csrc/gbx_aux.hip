@@ -427,18 +427,17 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
     // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
     const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
                           (((bgp >> 6) & 3u) << 24)) & bg_on;
+    // Samples x = 2 ox >= WX - 7 show the window: ox >= h = (WX - 6) >> 1,
+    // so byte i of group g when 4g + i >= h (h = 80, none, without it).
+    const int h8 = win ? 8 * ((wx7 + 1) >> 1) : 8 * kDsW;
     uint32_t word[kGroups] = {};
     uint32_t pword = 0;
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) {
       // colours of samples 4g..4g+3, one per byte
       uint32_t col = __builtin_amdgcn_alignbyte(cb[g + 1], cb[g], qb);
-      if (win) {
-        // samples x = 8g + 2i >= WX - 7 show the window
-        const int d = min(max((wx7 + 1 - 8 * g) >> 1, 0), 4);
-        const uint32_t m = d >= 4 ? 0u : (~0u << (8 * d));
-        col = (col & ~m) | (__builtin_amdgcn_alignbyte(cw[g + 1], cw[g], qw) & m);
-      }
+      const uint32_t m = (uint32_t)(~0ull << min(max(h8 - 32 * g, 0), 32));  // the window's bytes
+      col = (col & ~m) | (__builtin_amdgcn_alignbyte(cw[g + 1], cw[g], qw) & m);
       col &= bg_on;
       uint32_t shade = __builtin_amdgcn_perm(0u, pbg, col);
       const uint2 ob = *reinterpret_cast<const uint2*>(&obj[g][tid][0]);
