@@ -119,6 +119,17 @@ __device__ __forceinline__ uint32_t spread_tile(uint32_t t, uint32_t p) {
   return ev | od;
 }
 
+// The colours of the four sampled pixels p, p + 2, p + 4, p + 6 (p = 0 or 1,
+// from the left) of a sprite's tile row t = lo | hi << 8, one per byte,
+// mirrored with xflip: pixel j is bit 7 - j of lo and hi, or bit j.
+__device__ __forceinline__ uint32_t sprite_colours(uint32_t t, uint32_t p, uint32_t xflip) {
+  if (!xflip) return spread_tile(t, p);
+  const uint32_t u = ((t >> p) & 0x55u) | ((t >> (7u + p)) & 0xAAu);
+  const uint32_t ev = ((u & 0x33u) * 0x1001u) & 0x00030003u;
+  const uint32_t od = ((u & 0xCCu) * 0x40040u) & 0x03000300u;
+  return ev | od;
+}
+
 // One BG or window layer of a row, for a layer whose sample x reads map pixel
 // px = (x + s) & 0xFF (s = SCX for the background, 7 - WX for the window):
 // c[j] = the sampled colours (spread_tile) of map column ((s >> 3) + j) & 31.
@@ -374,18 +385,29 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
           const uint32_t attr = ent[t] >> 24;
           const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
           const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
-          const int left = (int)sx - 8;
-          // the sampled columns x = 2*ox inside [left, left + 8)
-          for (int x = (left + 1) & ~1; x < left + 8; x += 2) {
-            if (x < 0 || x >= 2 * kDsW) continue;
-            const uint32_t pxl = (uint32_t)(x - left);
-            const uint32_t bit = ((attr >> 5) & 1u) ? pxl : 7u - pxl;
-            const uint32_t color = (((hi[t] >> bit) & 1u) << 1) | ((lo[t] >> bit) & 1u);
-            if (color == 0) continue;
-            const uint32_t ox = (uint32_t)x >> 1;
-            uint16_t& slot = obj[ox >> 2][tid][ox & 3u];
-            const uint32_t cur = slot;
-            if (cur == 0 || sx < (cur >> 8)) slot = (uint16_t)(tag | ((pal >> (color * 2u)) & 3u));
+          // The sampled columns x = 2 ox inside [sx - 8, sx): ox0 .. ox0 + 3,
+          // the sprite's pixels p + 2i (p = sx & 1), colours one per byte.
+          // The four slots are distinct, so all four are read, then all four
+          // written (the old entry where the sample does not change it).  A
+          // sample off the screen uses a slot next to the sprite's (ox0 + 4
+          // or ox0 - 1, on the screen and none of its four) and writes that
+          // slot's own entry back.
+          const int ox0 = ((int)sx - 7) >> 1;
+          const uint32_t cols = sprite_colours(lo[t] | (hi[t] << 8), sx & 1u, (attr >> 5) & 1u);
+          uint32_t addr[4], cur[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ox = ox0 + i;
+            const uint32_t o = (uint32_t)ox < (uint32_t)kDsW ? (uint32_t)ox : (uint32_t)(ox0 < 0 ? ox0 + 4 : ox0 - 1);
+            addr[i] = __umul24(o >> 2, (uint32_t)(kImgThreads * 4)) + (o & 3u);
+            cur[i] = (&obj[0][tid][0])[addr[i]];
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t c = (cols >> (8 * i)) & 3u;
+            const bool upd = ((uint32_t)(ox0 + i) < (uint32_t)kDsW) & (c != 0u) &
+                             ((cur[i] == 0u) | (sx < (cur[i] >> 8)));
+            (&obj[0][tid][0])[addr[i]] = (uint16_t)(upd ? tag | ((pal >> (c * 2u)) & 3u) : cur[i]);
           }
         }
       }
