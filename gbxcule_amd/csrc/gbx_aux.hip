@@ -257,8 +257,8 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
   };
   uint32_t blk, part;
   using K0 = std::integral_constant<int, 0>;
-  using K3 = std::integral_constant<int, 3>;
-  using K8 = std::integral_constant<int, 8>;
+  using K4 = std::integral_constant<int, 4>;
+  using K10 = std::integral_constant<int, 10>;
   using KN = std::integral_constant<int, kImgLoads>;
   group(0u, blk, part);
   fetch(blk, part, 0x1FFu, K0{}, KN{});
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       if (i < kImgRows) *reinterpret_cast<uint2*>(img + (size_t)i * kImgEnvs) = v[k];
     }
     // The next group's rows load while this one renders, in three parts:
-    // loads 0-2 once the coverage is marked, 3-7 after the sprites, 8-14
+    // loads 0-3 once the coverage is marked, 4-9 after the sprites, 10-14
     // after the BG and window layers (their tile rows then no longer hold
     // registers).  Issued at once, the loads of the 9 wavefronts queue in
     // the CU's memory pipeline and hold each wavefront at the issue of its
@@ -329,7 +329,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       }
     }
     __syncthreads();
-    if (more) fetch(nblk_next, npart, need, K0{}, K3{});
+    if (more) fetch(nblk_next, npart, need, K0{}, K4{});
     const uint32_t lcdc = r.reg(0xFF40);
     const uint32_t height = (lcdc & 0x04u) ? 16u : 8u;
     const uint32_t scy = r.reg(0xFF42), scx = r.reg(0xFF43);
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       }
     }
 
-    if (more) fetch(nblk_next, npart, need, K3{}, K8{});
+    if (more) fetch(nblk_next, npart, need, K4{}, K10{});
     const uint32_t bg_on = (lcdc & 0x01u) ? ~0u : 0u;
     const bool win = (lcdc & 0x20u) && y >= wy;
     const int wx7 = (int)wx - 7;
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
         layer_tiles(r, lcdc, sw, pyw, id, cw);
       }
     }
-    if (more) fetch(nblk_next, npart, need, K8{}, KN{});
+    if (more) fetch(nblk_next, npart, need, K10{}, KN{});
     const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
     // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
     const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
