@@ -122,9 +122,11 @@ __device__ __forceinline__ uint32_t spread_tile(uint32_t t, uint32_t p) {
 // The colours of the four sampled pixels p, p + 2, p + 4, p + 6 (p = 0 or 1,
 // from the left) of a sprite's tile row t = lo | hi << 8, one per byte,
 // mirrored with xflip: pixel j is bit 7 - j of lo and hi, or bit j.
-__device__ __forceinline__ uint32_t sprite_colours(uint32_t t, uint32_t p, uint32_t xflip) {
-  if (!xflip) return spread_tile(t, p);
-  const uint32_t u = ((t >> p) & 0x55u) | ((t >> (7u + p)) & 0xAAu);
+__device__ __forceinline__ uint32_t sprite_colours(uint32_t t, uint32_t p, bool xflip) {
+  // unmirrored as spread_tile; mirrored, lo bit p + 2i and hi bit 8 + p + 2i
+  // to bits 2i and 2i + 1 of u directly
+  const uint32_t src = xflip ? t : __builtin_bitreverse32(t);
+  const uint32_t u = ((src >> (p + (xflip ? 0u : 24u))) & 0x55u) | ((src >> (p + (xflip ? 7u : 15u))) & 0xAAu);
   const uint32_t ev = ((u & 0x33u) * 0x1001u) & 0x00030003u;
   const uint32_t od = ((u & 0xCCu) * 0x40040u) & 0x03000300u;
   return ev | od;
@@ -191,10 +193,10 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
   static_assert(kImgBytes % 16 == 0, "the sprite line buffer stays 16-byte aligned");
   __shared__ uint4 lds[(kImgBytes + kObjBytes + (size_t)kDsH * kImgEnvs * sizeof(uint64_t)) / 16];
   uint8_t* const img = reinterpret_cast<uint8_t*>(lds);
-  // sprite line buffer, 4 samples per (group, thread): 0 = no sprite pixel,
-  // else bits [0:1] its shade (palette applied), [2] behind non-zero BG, [3]
-  // set, [8:15] the sprite's OAM x (its left edge + 8); reused as the
-  // output stage
+  // sprite line buffer, 4 samples per (group, thread): bits [0:1] the
+  // sample's sprite shade (palette applied), [2] behind non-zero BG, [3] set
+  // (a sprite pixel), [8:15] that sprite's OAM x (its left edge + 8), 0xFF00
+  // while no sprite pixel is set; reused as the output stage
   auto obj = reinterpret_cast<uint16_t(*)[kImgThreads][4]>(img + kImgBytes);
   // OAM entries covering each (env, output row): bit k = entry k
   auto cover = reinterpret_cast<uint64_t(*)[kImgEnvs]>(img + kImgBytes + kObjBytes);
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
     const uint32_t oy = rblk * 8u + ((tid >> 3) & 7u);
     const uint32_t y = oy * 2u;
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&obj[g][tid][0]) = make_uint2(0u, 0u);
+    for (int g = 0; g < kGroups; ++g) *reinterpret_cast<uint2*>(&obj[g][tid][0]) = make_uint2(0xFF00FF00u, 0xFF00FF00u);
     cover[oy][env] = 0u;
     __syncthreads();
     const Img r{img, env};
@@ -335,6 +337,11 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
     const uint32_t scy = r.reg(0xFF42), scx = r.reg(0xFF43);
     const uint32_t bgp = r.reg(0xFF47), obp0 = r.reg(0xFF48), obp1 = r.reg(0xFF49);
     const uint32_t wy = r.reg(0xFF4A), wx = r.reg(0xFF4B);
+    // OBP0 and OBP1 as byte tables: byte c = shade of colour c
+    const uint32_t ptab0 = (obp0 & 3u) | (((obp0 >> 2) & 3u) << 8) | (((obp0 >> 4) & 3u) << 16) |
+                           (((obp0 >> 6) & 3u) << 24);
+    const uint32_t ptab1 = (obp1 & 3u) | (((obp1 >> 2) & 3u) << 8) | (((obp1 >> 4) & 3u) << 16) |
+                           (((obp1 >> 6) & 3u) << 24);
     if (lcdc & 0x02u) {
       // the entries covering this row (position valid, row inside their 8 or
       // 16 lines) in OAM order, then only the first 10
@@ -383,31 +390,32 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
           if (!on[t]) continue;
           const uint32_t sx = (ent[t] >> 8) & 0xFFu;
           const uint32_t attr = ent[t] >> 24;
-          const uint32_t pal = ((attr >> 4) & 1u) ? obp1 : obp0;
           const uint32_t tag = (sx << 8) | 0x08u | (((attr >> 7) & 1u) << 2);
           // The sampled columns x = 2 ox inside [sx - 8, sx): ox0 .. ox0 + 3,
           // the sprite's pixels p + 2i (p = sx & 1), colours one per byte.
-          // The four slots are distinct, so all four are read, then all four
-          // written (the old entry where the sample does not change it).  A
-          // sample off the screen uses a slot next to the sprite's (ox0 + 4
-          // or ox0 - 1, on the screen and none of its four) and writes that
-          // slot's own entry back.
+          // They go to the four slots from oc = ox0 clamped to [0, 76],
+          // sample i to slot i + ox0 - oc: a sample off the screen falls
+          // outside the four, its colour byte shifted out (transparent).
+          // The slots are distinct, so all four are read, then all four
+          // written (the old entry where the sample does not change it).
           const int ox0 = ((int)sx - 7) >> 1;
-          const uint32_t cols = sprite_colours(lo[t] | (hi[t] << 8), sx & 1u, (attr >> 5) & 1u);
-          uint32_t addr[4], cur[4];
+          const int oc = min(max(ox0, 0), kDsW - 4), d = ox0 - oc;  // d in -3 .. 4
+          const uint32_t c0 = sprite_colours(lo[t] | (hi[t] << 8), sx & 1u, ((attr >> 5) & 1u) != 0u);
+          const uint32_t cols = (uint32_t)(((uint64_t)c0 << 32) >> (32 - 8 * d));  // c0 shifted by 8d
+          const uint32_t shades = __builtin_amdgcn_perm(0u, ((attr >> 4) & 1u) ? ptab1 : ptab0, cols);
+          const uint32_t q = (uint32_t)oc & 3u;
+          uint16_t* const w0 = &obj[0][tid][q] + __umul24((uint32_t)oc >> 2, 4u * (uint32_t)kImgThreads);
+          uint16_t* slot[4];
+          uint32_t cur[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int ox = ox0 + i;
-            const uint32_t o = (uint32_t)ox < (uint32_t)kDsW ? (uint32_t)ox : (uint32_t)(ox0 < 0 ? ox0 + 4 : ox0 - 1);
-            addr[i] = __umul24(o >> 2, (uint32_t)(kImgThreads * 4)) + (o & 3u);
-            cur[i] = (&obj[0][tid][0])[addr[i]];
+          for (int j = 0; j < 4; ++j) {
+            slot[j] = w0 + j + (q + (uint32_t)j >= 4u ? 4 * kImgThreads - 4 : 0);  // the next group's
+            cur[j] = *slot[j];
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t c = (cols >> (8 * i)) & 3u;
-            const bool upd = ((uint32_t)(ox0 + i) < (uint32_t)kDsW) & (c != 0u) &
-                             ((cur[i] == 0u) | (sx < (cur[i] >> 8)));
-            (&obj[0][tid][0])[addr[i]] = (uint16_t)(upd ? tag | ((pal >> (c * 2u)) & 3u) : cur[i]);
+          for (int j = 0; j < 4; ++j) {
+            const bool upd = (((cols >> (8 * j)) & 3u) != 0u) & (sx < (cur[j] >> 8));  // empty: x 0xFF
+            *slot[j] = (uint16_t)(upd ? tag | ((shades >> (8 * j)) & 3u) : cur[j]);
           }
         }
       }
