@@ -77,6 +77,7 @@ constexpr int kImgLoads = (int)((kImgRows + kImgThreads - 1) / kImgThreads);
 constexpr int kTileSlots = 21;     // tile columns one 80-sample row can touch
 constexpr int kGroups = kDsW / 4;  // 4-sample groups per row (one output word unpacked)
 static_assert(kImgEnvs == 8, "image rows are 8 bytes");
+static_assert((kImgLoads - 1) * kImgThreads <= (int)kImgVram, "the OAM rows come from the last load");
 
 // The image rows that four envs' renders read, from their LCDC bytes x, as
 // a mask of 1 KiB video RAM chunks (bit c: 8000 + 400h * c .. + 3FFh) and
@@ -101,7 +102,11 @@ struct Img {
   __device__ uint32_t M(uint32_t addr) const { return p[((addr - 0x8000u) << 3) | env]; }  // video RAM
   __device__ uint32_t off(uint32_t addr) const { return ((addr - 0x8000u) << 3) | env; }  // M's byte
   __device__ uint32_t at(uint32_t o) const { return p[o]; }
-  __device__ uint32_t oam(uint32_t i) const { return p[((kImgVram + i) << 3) | env]; }
+  // OAM is stored per env (the image's OAM rows transposed): env e's 160
+  // bytes from byte 8 * 2000h + 160 e, entry k one aligned word
+  __device__ uint32_t oam_entry(uint32_t k) const {
+    return *reinterpret_cast<const uint32_t*>(p + (kImgVram << 3) + env * kImgOam + 4u * k);
+  }
   __device__ uint32_t reg(uint32_t addr) const { return p[((kImgVram + kImgOam + addr - 0xFF40u) << 3) | env]; }
 };
 
@@ -280,7 +285,15 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
 #pragma unroll
     for (int k = 0; k < kImgLoads; ++k) {
       const uint32_t i = tid + (uint32_t)k * kImgThreads;
-      if (i < kImgRows) *reinterpret_cast<uint2*>(img + (size_t)i * kImgEnvs) = v[k];
+      if (k == kImgLoads - 1 && i - kImgVram < kImgOam) {
+        // an OAM row: its 8 envs' bytes to their per-env OAM copies
+#pragma unroll
+        for (int e = 0; e < kImgEnvs; ++e)
+          img[(kImgVram << 3) + (uint32_t)e * kImgOam + (i - kImgVram)] =
+              (uint8_t)((e < 4 ? v[k].x : v[k].y) >> (8 * (e & 3)));
+      } else if (i < kImgRows) {
+        *reinterpret_cast<uint2*>(img + (size_t)i * kImgEnvs) = v[k];
+      }
     }
     // The next group's rows load while this one renders, in three parts:
     // loads 0-3 once the coverage is marked, 4-9 after the sprites, 10-14
@@ -318,7 +331,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
     if (tid < 40u * (uint32_t)kImgEnvs) {
       const uint32_t e = tid / 40u, k = tid % 40u;
       const Img o{img, e};
-      const uint32_t sy = o.oam(4u * k), sx = o.oam(4u * k + 1u);
+      const uint32_t oe = o.oam_entry(k), sy = oe & 0xFFu, sx = (oe >> 8) & 0xFFu;
       const uint32_t ht = (o.reg(0xFF40) & 0x04u) ? 16u : 8u;
       if ((sx != 0u) & (sy != 0u) & (sx < 168u) & (sy < 160u)) {
         const uint32_t first = (sy > 16u ? sy - 16u : 0u) >> 1;
@@ -363,8 +376,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
           on[t] = vis != 0u;
           const uint32_t k = on[t] ? (uint32_t)__builtin_ctzll(vis) : 0u;
           vis &= vis - 1u;
-          ent[t] = r.oam(4u * k) | (r.oam(4u * k + 1u) << 8) | (r.oam(4u * k + 2u) << 16) |
-                   (r.oam(4u * k + 3u) << 24);
+          ent[t] = r.oam_entry(k);
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
