@@ -380,22 +380,16 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const uint32_t sy = ent[t] & 0xFFu;
-          const int top = (int)sy - 16;
-          uint32_t tile = (ent[t] >> 16) & 0xFFu;
-          const uint32_t attr = ent[t] >> 24;
-          uint32_t row = (uint32_t)((int)y - top) & 15u;
-          if ((attr >> 6) & 1u) row = (height - 1u - row) & 15u;
-          if (height == 16u) {
-            tile &= 0xFEu;
-            if (row >= 8u) {
-              tile += 1u;
-              row -= 8u;
-            }
-          }
-          const uint32_t ta = 0x8000u + tile * 16u + (row & 7u) * 2u;
-          lo[t] = on[t] ? r.M(ta) : 0u;
-          hi[t] = on[t] ? r.M(ta + 1u) : 0u;
+          // the sprite's line for this row, mirrored with y-flip; 8x16: the
+          // even tile above, the odd one below.  (A lane without a second
+          // entry reads entry 0's row and skips the merge.)
+          const uint32_t sy = ent[t] & 0xFFu, attr = ent[t] >> 24;
+          uint32_t row = (y + 16u - sy) & 15u;
+          row = ((attr >> 6) & 1u) ? (height - 1u - row) & 15u : row;
+          const uint32_t tile = height == 16u ? ((ent[t] >> 16) & 0xFEu) | (row >> 3) : (ent[t] >> 16) & 0xFFu;
+          const uint32_t o = r.off(0x8000u) + (tile << 7) + ((row & 7u) << 4);  // the row's low byte
+          lo[t] = r.at(o);
+          hi[t] = r.at(o + 8u);
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
