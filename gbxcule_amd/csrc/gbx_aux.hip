@@ -173,10 +173,10 @@ __device__ __forceinline__ void layer_tiles(const Img& r, uint32_t lcdc, uint32_
 // then renders one (env, output row) per thread.  Each image load brings a
 // 128-byte line for 16 useful bytes, so the CU's supply of L1 misses, not
 // HBM, bounds the copy: fewer lines and loads spread over the group are
-// what speed it up.  The 8 workgroups of a 64-env block are
-// dealt to one XCD (the hardware deals workgroup i to XCD i mod 8), so each
-// 64-byte line comes from HBM about once and its other reads hit that XCD's
-// L2.  Per row, the sprites (the first 10 OAM entries covering the line,
+// what speed it up.  The 8 workgroups of a 64-env block are dealt to one
+// XCD (the hardware deals workgroup i to XCD i mod 8), so each 64-byte line
+// comes from HBM about once and its other reads hit that XCD's L2.  Per
+// row, the sprites (the first 10 OAM entries covering the line,
 // counted before the x test) are resolved into a line buffer of the 80
 // samples: each sample keeps the opaque sprite pixel with the lowest x
 // (ties: the lower OAM index, the earlier entry), as the reference's
