@@ -729,19 +729,34 @@ __global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8
   }
 }
 
-__global__ void masked_state_kernel(DevState s, SnapState snap, const uint8_t* mask, int with_pix) {
-  const uint32_t e = blockIdx.x;  // one block per env, threads over bytes
-  if (e >= (uint32_t)s.n || !mask[e]) return;
-  const uint32_t t = threadIdx.x;
-  for (uint32_t i = t; i < (uint32_t)kSerialMax; i += blockDim.x)
-    s.serial[(size_t)e * kSerialMax + i] = snap.serial[i];
-  if (with_pix)
-    for (uint32_t i = t; i < (uint32_t)(kDsW * kDsH); i += blockDim.x)
-      s.pix[(size_t)e * kDsW * kDsH + i] = snap.pix[i];
-  if (t < (uint32_t)kCartStateStride) s.cs[cs_index(e, (int)t)] = snap.cs[t];
-  if (t < (uint32_t)kNumFields) s.sc[sc_index(e, (int)t)] = snap.sc[t];
-  if (t < 2u) s.cnt[cnt_index(e, (int)t)] = snap.cnt[t];
-  if (t == 0) s.actions[e] = snap.sc[F_ACTIONS];
+// One workgroup per 256 envs (a launch of one per env spent its time
+// dispatching workgroups that found their env unmasked): the masked envs
+// are listed in LDS, then each gets the snapshot's serial buffer, pixels
+// (16 bytes a thread), cart state, scalars, counters and action from the
+// whole workgroup.
+static_assert(kSerialMax % 16 == 0 && (kDsW * kDsH) % 16 == 0, "serial and pixel rows are 16-byte multiples");
+__global__ __launch_bounds__(256) void masked_state_kernel(DevState s, SnapState snap, const uint8_t* mask,
+                                                           int with_pix) {
+  __shared__ uint32_t list[256];
+  __shared__ uint32_t count;
+  const uint32_t t = threadIdx.x, e0 = blockIdx.x * 256u + t;
+  if (t == 0) count = 0;
+  __syncthreads();
+  if (e0 < (uint32_t)s.n && mask[e0]) list[atomicAdd(&count, 1u)] = e0;
+  __syncthreads();
+  const uint32_t m = count;
+  for (uint32_t i = 0; i < m; ++i) {
+    const uint32_t e = list[i];
+    for (uint32_t q = t; q < (uint32_t)kSerialMax / 16u; q += 256u)
+      reinterpret_cast<uint4*>(s.serial + (size_t)e * kSerialMax)[q] = reinterpret_cast<const uint4*>(snap.serial)[q];
+    if (with_pix)
+      for (uint32_t q = t; q < (uint32_t)(kDsW * kDsH) / 16u; q += 256u)
+        reinterpret_cast<uint4*>(s.pix + (size_t)e * kDsW * kDsH)[q] = reinterpret_cast<const uint4*>(snap.pix)[q];
+    if (t < (uint32_t)kCartStateStride) s.cs[cs_index(e, (int)t)] = snap.cs[t];
+    if (t < (uint32_t)kNumFields) s.sc[sc_index(e, (int)t)] = snap.sc[t];
+    if (t < 2u) s.cnt[cnt_index(e, (int)t)] = snap.cnt[t];
+    if (t == 0) s.actions[e] = snap.sc[F_ACTIONS];
+  }
 }
 
 // RAM senses: out[e*k + j] = raw byte addrs[j] of env e.
@@ -750,8 +765,21 @@ __global__ void gather_kernel(DevState s, const uint16_t* addrs, int k, uint8_t*
   if (e >= (uint32_t)s.n) return;
   const uint8_t* mb = s.mem + ((size_t)block_of(e) << 22);
   const uint32_t lane = e & (kEnvBlock - 1);
-  for (int j = 0; j < k; ++j)
-    out[(size_t)e * k + j] = mb[((size_t)addrs[j] << kEnvBlockShift) | lane];
+  auto byte = [&](int j) { return (uint32_t)mb[((size_t)addrs[j] << kEnvBlockShift) | lane]; };
+  if (((reinterpret_cast<uintptr_t>(out) | (uintptr_t)k) & 15u) == 0u) {
+    // the env's bytes 16-byte aligned: one 16-byte store per 16 (not one
+    // byte store per sense, 64 lanes k bytes apart)
+    for (int j0 = 0; j0 < k; j0 += 16) {
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        w[q] = byte(j0 + 4 * q) | (byte(j0 + 4 * q + 1) << 8) | (byte(j0 + 4 * q + 2) << 16) |
+               (byte(j0 + 4 * q + 3) << 24);
+      *reinterpret_cast<uint4*>(out + (size_t)e * k + j0) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  } else {
+    for (int j = 0; j < k; ++j) out[(size_t)e * k + j] = (uint8_t)byte(j);
+  }
 }
 
 // Per-env linear hash: sum of byte * K[addr] over memory, plus the scalar
@@ -933,8 +961,8 @@ hipError_t launch_masked_reset(const DevState& s, const SnapState& snap, const u
   const uint32_t chunks = (restore_rows((uint32_t)s.cram_stride, live != 0) + kResetRows - 1) / kResetRows;
   hipLaunchKernelGGL(masked_mem_kernel, dim3((unsigned)((s.n + kEnvBlock - 1) / kEnvBlock), chunks),
                      dim3(256), 0, st, s, snap.mem, snap.cram, mask, live);
-  hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)s.n), dim3(256), 0, st, s, snap, mask,
-                     snap.has_pix);
+  hipLaunchKernelGGL(masked_state_kernel, dim3((unsigned)((s.n + 255) / 256)), dim3(256), 0, st, s, snap,
+                     mask, snap.has_pix);
   return hipGetLastError();
 }
 
