@@ -485,10 +485,20 @@ class HipVecBackend:
         return self.memory_torch()[env_idx, lo:hi]
 
     def ram_senses_torch(self, addrs, out=None):
-        """``out[e, j] = mem[e][addrs[j]]`` for all envs in one launch."""
+        """``out[e, j] = mem[e][addrs[j]]`` for all envs in one launch.  Host
+        address lists are uploaded once and reused while the same list comes
+        back (an RL loop passes one fixed list every step)."""
         torch = _torch()
-        a = torch.as_tensor(addrs, dtype=torch.int32).to(torch.int16)
-        a = a.to(device="cuda").contiguous()
+        if isinstance(addrs, torch.Tensor):
+            a = addrs.to(torch.int32).to(torch.int16).to(device="cuda").contiguous()
+        else:
+            key = np.asarray(addrs, dtype=np.int64).tobytes()
+            cached = getattr(self, "_senses_addrs", None)
+            if cached is not None and cached[0] == key:
+                a = cached[1]
+            else:
+                a = torch.as_tensor(addrs, dtype=torch.int32).to(torch.int16).to(device="cuda").contiguous()
+                self._senses_addrs = (key, a)
         k = int(a.numel())
         if out is None:
             out = torch.empty((self.num_envs, k), dtype=torch.uint8, device="cuda")

@@ -181,3 +181,33 @@ def test_dead_rows_restored_exactly_when_changed(bootstub, route):
     finally:
         dut.close()
         ref.close()
+
+
+def test_ram_senses_address_lists(carts, bootstub):
+    """``ram_senses_torch`` keeps the last host address list on the device;
+    a changed list, a list changed in place, a repeated one and a device
+    tensor must each read the bytes ``export_memory`` returns, and a 16-byte
+    multiple of senses (the 16-byte store path) and an odd count (the byte
+    path) both."""
+    require_gpu()
+    import torch
+
+    n = 130  # three memory blocks, the last partly padding
+    dut = _backend(carts["c3"], bootstub, n)
+    try:
+        dut.reset(seed=0)
+        for k in range(2):
+            dut.step(seeded_actions(3, k, n))
+        mem = dut.export_memory()
+        rng = np.random.default_rng(5)
+        a = np.sort(rng.choice(np.arange(0x8000, 0x10000), 32, replace=False))
+        b = np.sort(rng.choice(np.arange(0xC000, 0xE000), 7, replace=False))
+        c = a.copy()
+        for addrs in (a, b, a, c, torch.as_tensor(b.astype(np.int32), device="cuda")):
+            got = dut.ram_senses_torch(addrs).cpu().numpy()
+            want = mem[:, np.asarray(addrs.cpu() if isinstance(addrs, torch.Tensor) else addrs)]
+            np.testing.assert_array_equal(got, want)
+        c[3] ^= 0x0100  # the same array object, changed in place
+        np.testing.assert_array_equal(dut.ram_senses_torch(c).cpu().numpy(), mem[:, c])
+    finally:
+        dut.close()
