@@ -73,11 +73,29 @@ constexpr uint32_t kImgOam = 0xA0u;     // FE00-FE9F
 constexpr uint32_t kImgRegs = 0x0Cu;    // FF40-FF4B
 constexpr uint32_t kImgRows = kImgVram + kImgOam + kImgRegs;
 constexpr int kImgThreads = kImgEnvs * kDsH;  // one per (env, output row)
-constexpr int kImgLoads = (int)((kImgRows + kImgThreads - 1) / kImgThreads);
+// The 9 wavefronts of a workgroup sit on the 4 SIMDs as w mod 4, so SIMD 0
+// carries three.  Loads 0 .. kImgLoadsAll-1 of the image come from every
+// thread (rows 576k + tid); the rest only from the six wavefronts off SIMD 0
+// (384 rows per load), which leaves SIMD 0's three with fewer to issue.
+constexpr int kImgLoadsAll = 8;
+constexpr int kImgFetchThreads = 384;
+constexpr uint32_t kImgRowsAll = (uint32_t)kImgLoadsAll * kImgThreads;
+constexpr int kImgLoads =
+    kImgLoadsAll + (int)((kImgRows - kImgRowsAll + kImgFetchThreads - 1) / kImgFetchThreads);
 constexpr int kTileSlots = 21;     // tile columns one 80-sample row can touch
 constexpr int kGroups = kDsW / 4;  // 4-sample groups per row (one output word unpacked)
 static_assert(kImgEnvs == 8, "image rows are 8 bytes");
-static_assert((kImgLoads - 1) * kImgThreads <= (int)kImgVram, "the OAM rows come from the last load");
+static_assert(kImgThreads == 9 * 64 && kImgFetchThreads == 6 * 64, "nine wavefronts, six off SIMD 0");
+// First image row of load k for wavefront w (of all nine with k below
+// kImgLoadsAll, else fetch wavefront fw = w - 1 - w/4 of the six); the
+// wavefront's 64 lanes take the 64 rows from there.
+__host__ __device__ constexpr uint32_t img_row_base(int k, uint32_t w) {
+  return k < kImgLoadsAll ? (uint32_t)k * kImgThreads + w * 64u
+                          : kImgRowsAll + (uint32_t)(k - kImgLoadsAll) * kImgFetchThreads +
+                                (w - 1u - (w >> 2)) * 64u;
+}
+static_assert(kImgRowsAll <= kImgVram && img_row_base(kImgLoads - 1, 1) <= kImgVram,
+              "only the last load reaches past video RAM, and it holds every OAM row");
 
 // The image rows that four envs' renders read, from their LCDC bytes x, as
 // a mask of 1 KiB video RAM chunks (bit c: 8000 + 400h * c .. + 3FFh) and
@@ -233,25 +251,36 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
   // returns zeros without a memory request (a branch around the load would
   // make the compiler drain every outstanding load before the next one).
   uint2 v[kImgLoads];
-  const uint32_t wrow = __builtin_amdgcn_readfirstlane(tid0 >> 6) * 64u;
+  // wavefront index; those with w mod 4 != 0 (off SIMD 0) take the loads
+  // past kImgLoadsAll
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   auto fetch = [&](uint32_t blk, uint32_t part, uint32_t need, auto k0, auto k1) {
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         s.mem + ((size_t)blk << 22), 0, 1 << 22, 0x00020000);  // untyped raw buffer
-    // (recomputed per call: kept across the loop, the 15 offsets would hold
+    // (recomputed per call: kept across the loop, the offsets would hold
     // registers the render needs)
-    uint32_t t = tid0;
-    asm volatile("" : "+v"(t));
-    __builtin_assume(t < (uint32_t)kImgThreads);  // only the last load reaches past video RAM
-#pragma unroll
-    for (int k = decltype(k0)::value; k < decltype(k1)::value; ++k) {
-      const uint32_t i = min(t + (uint32_t)k * kImgThreads, kImgRows - 1u);
-      const uint32_t a = i < kImgVram ? 0x8000u + i
-                         : i < kImgVram + kImgOam ? 0xFE00u + (i - kImgVram)
-                                                  : 0xFF40u + (i - kImgVram - kImgOam);
-      const bool want = (need >> ((wrow + (uint32_t)k * kImgThreads) >> 10)) & 1u;
+    uint32_t t = tid0, w = wv;
+    asm volatile("" : "+v"(t), "+s"(w));
+    const uint32_t f = t - 64u - ((w >> 2) << 6);  // row of load kImgLoadsAll, less kImgRowsAll
+    auto one = [&](int k) {
+      const uint32_t r0 = img_row_base(k, w);
+      const uint32_t i0 = k < kImgLoadsAll ? t + (uint32_t)k * kImgThreads
+                                           : f + img_row_base(k, 1u);
+      const uint32_t i = k == kImgLoads - 1 ? min(i0, kImgRows - 1u) : i0;
+      const uint32_t a = k < kImgLoads - 1 || i < kImgVram ? 0x8000u + i
+                         : i < kImgVram + kImgOam          ? 0xFE00u + (i - kImgVram)
+                                                           : 0xFF40u + (i - kImgVram - kImgOam);
+      const bool want = (need >> (r0 >> 10)) & 1u;
       const auto w = __builtin_amdgcn_raw_buffer_load_b64(rb, (int)(want ? a << kEnvBlockShift : 0x80000000u),
                                                           (int)(part * (uint32_t)kImgEnvs), 0);
       v[k] = make_uint2(w[0], w[1]);
+    };
+    constexpr int a0 = decltype(k0)::value, a1 = decltype(k1)::value;
+#pragma unroll
+    for (int k = a0; k < (a1 < kImgLoadsAll ? a1 : kImgLoadsAll); ++k) one(k);
+    if ((w & 3u) != 0u) {
+#pragma unroll
+      for (int k = a0 > kImgLoadsAll ? a0 : kImgLoadsAll; k < a1; ++k) one(k);
     }
   };
   // a group's 8 LCDC bytes (one broadcast load), for its chunk mask
@@ -280,27 +309,34 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
   for (uint32_t it = 0; it < rounds; ++it) {
     // (derived per round: kept across the loop, the addresses that follow
     // from the thread index would hold registers the render needs)
-    uint32_t tid = tid0;
-    asm volatile("" : "+v"(tid));
-#pragma unroll
-    for (int k = 0; k < kImgLoads; ++k) {
-      const uint32_t i = tid + (uint32_t)k * kImgThreads;
+    uint32_t tid = tid0, w = wv;
+    asm volatile("" : "+v"(tid), "+s"(w));
+    const uint32_t f = tid - 64u - ((w >> 2) << 6);
+    auto put = [&](int k) {
+      const uint32_t i = k < kImgLoadsAll ? tid + (uint32_t)k * kImgThreads : f + img_row_base(k, 1u);
       if (k == kImgLoads - 1 && i - kImgVram < kImgOam) {
         // an OAM row: its 8 envs' bytes to their per-env OAM copies
 #pragma unroll
         for (int e = 0; e < kImgEnvs; ++e)
           img[(kImgVram << 3) + (uint32_t)e * kImgOam + (i - kImgVram)] =
               (uint8_t)((e < 4 ? v[k].x : v[k].y) >> (8 * (e & 3)));
-      } else if (i < kImgRows) {
+      } else if (k < kImgLoads - 1 || i < kImgRows) {
         *reinterpret_cast<uint2*>(img + (size_t)i * kImgEnvs) = v[k];
       }
+    };
+#pragma unroll
+    for (int k = 0; k < kImgLoadsAll; ++k) put(k);
+    if ((w & 3u) != 0u) {
+#pragma unroll
+      for (int k = kImgLoadsAll; k < kImgLoads; ++k) put(k);
     }
     // The next group's rows load while this one renders, in three parts:
-    // loads 0-3 once the coverage is marked, 4-9 after the sprites, 10-14
-    // after the BG and window layers (their tile rows then no longer hold
-    // registers).  Issued at once, the loads of the 9 wavefronts queue in
-    // the CU's memory pipeline and hold each wavefront at the issue of its
-    // last one; spread over the group, they stream beside the render.
+    // loads 0-3 once the coverage is marked, 4-9 after the sprites, the
+    // rest after the BG and window layers (their tile rows then no longer
+    // hold registers); SIMD 0's wavefronts stop at load 7.  Issued at once,
+    // the loads of the 9 wavefronts queue in the CU's memory pipeline and
+    // hold each wavefront at the issue of its last one; spread over the
+    // group, they stream beside the render.
     uint32_t nblk_next = 0, npart = 0, need = 0;
     const bool more = it + 1u < rounds;
     if (more) {
