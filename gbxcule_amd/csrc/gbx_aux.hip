@@ -294,7 +294,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
   uint32_t blk, part;
   using K0 = std::integral_constant<int, 0>;
   using K4 = std::integral_constant<int, 4>;
-  using K10 = std::integral_constant<int, 10>;
+  using K8 = std::integral_constant<int, kImgLoadsAll>;
   using KN = std::integral_constant<int, kImgLoads>;
   group(0u, blk, part);
   fetch(blk, part, 0x1FFu, K0{}, KN{});
@@ -331,9 +331,9 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       for (int k = kImgLoadsAll; k < kImgLoads; ++k) put(k);
     }
     // The next group's rows load while this one renders, in three parts:
-    // loads 0-3 once the coverage is marked, 4-9 after the sprites, the
-    // rest after the BG and window layers (their tile rows then no longer
-    // hold registers); SIMD 0's wavefronts stop at load 7.  Issued at once,
+    // loads 0-3 once the coverage is marked, 4-7 after the sprites (the last
+    // of SIMD 0's wavefronts), the rest after the BG and window layers (their
+    // tile rows then no longer hold registers).  Issued at once,
     // the loads of the 9 wavefronts queue in the CU's memory pipeline and
     // hold each wavefront at the issue of its last one; spread over the
     // group, they stream beside the render.
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       }
     }
 
-    if (more) fetch(nblk_next, npart, need, K4{}, K10{});
+    if (more) fetch(nblk_next, npart, need, K4{}, K8{});
     const uint32_t bg_on = (lcdc & 0x01u) ? ~0u : 0u;
     const bool win = (lcdc & 0x20u) && y >= wy;
     const int wx7 = (int)wx - 7;
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
         layer_tiles(r, lcdc, sw, pyw, id, cw);
       }
     }
-    if (more) fetch(nblk_next, npart, need, K10{}, KN{});
+    if (more) fetch(nblk_next, npart, need, K8{}, KN{});
     const uint32_t qb = (scx & 7u) >> 1, qw = (sw & 7u) >> 1;
     // BGP as a byte table: byte c = shade of colour c (all zero with the BG off)
     const uint32_t pbg = ((bgp & 3u) | (((bgp >> 2) & 3u) << 8) | (((bgp >> 4) & 3u) << 16) |
