@@ -9,6 +9,19 @@
 namespace gbx {
 namespace {
 
+// Streams that pass through once (the masked restore's rows, the render's
+// output) go through nontemporal loads and stores, which leave the lines
+// the next kernels reuse (records, ROM, the envs' memory rows) in L2.
+typedef uint32_t nt4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const nt4 q = __builtin_nontemporal_load(reinterpret_cast<const nt4*>(p));
+  return make_uint4(q[0], q[1], q[2], q[3]);
+}
+__device__ __forceinline__ void st_stream(uint4* p, uint4 v) {
+  const nt4 q = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(q, reinterpret_cast<nt4*>(p));
+}
+
 __device__ __forceinline__ uint32_t block_of(uint32_t e) {
   return __builtin_amdgcn_readfirstlane(e >> kEnvBlockShift);
 }
@@ -552,8 +565,8 @@ __global__ __launch_bounds__(kImgThreads) void render_kernel(DevState s, uint8_t
       for (uint32_t d = 4u * lane; d < 64u * nw; d += 256u) {
         const uint32_t e = d / (8u * nw), w2 = d % (8u * nw);
         if (env0 + e < (uint32_t)s.n)
-          *reinterpret_cast<uint4*>(out + base + (size_t)(env0 + e) * env_bytes + rblk * 32u * nw + 4u * w2) =
-              *reinterpret_cast<const uint4*>(stage(d));
+          st_stream(reinterpret_cast<uint4*>(out + base + (size_t)(env0 + e) * env_bytes + rblk * 32u * nw + 4u * w2),
+                    *reinterpret_cast<const uint4*>(stage(d)));
       }
     } else {
       const bool aligned = (ob & 3u) == 0u;
@@ -747,7 +760,7 @@ __global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8
                             : s.cram + ((cram_base + off) << kEnvBlockShift);
       p[i] = ok ? reinterpret_cast<uint4*>(row) + k : nullptr;
       w[i] = (ok ? (uint32_t)(in_mem ? snap_mem[ri] : snap_cram[off]) : 0u) * 0x01010101u;
-      cur[i] = ok ? *p[i] : make_uint4(0, 0, 0, 0);
+      cur[i] = ok ? ld_stream(p[i]) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < kResetBatch; ++i) {
@@ -760,7 +773,7 @@ __global__ __launch_bounds__(256) void masked_mem_kernel(DevState s, const uint8
       // the row changed if any of its quad's lanes changed (quad_perm OR)
       d |= (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0xB1, 0xF, 0xF, true);
       d |= (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0x4E, 0xF, 0xF, true);
-      if (p[i] != nullptr && d != 0u) *p[i] = nv;
+      if (p[i] != nullptr && d != 0u) st_stream(p[i], nv);
     }
   }
 }
